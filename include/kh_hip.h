@@ -1,0 +1,142 @@
+/*
+ * kh_hip.h — C ABI of libkh_hip.so, the MI355X (gfx950) executor of kleinhirn encoder plans.
+ *
+ * The library is the device side of a `Backend` / `PlanRunner` pair (src/backend.ts:14-46 of the
+ * reference). A host (hip-backend.ts over Node-API, or Python over ctypes) hands it the weights
+ * of a manifest, then plans as JSON, then per call the RunInput arrays. Plain pointers and sizes
+ * only; every entry point returns KH_OK (0) or an error code, and kh_last_error() gives the
+ * message of the calling thread's last failure.
+ *
+ * Execution model: a plan's rows are stored packed (the valid rows of each sequence back to back,
+ * cu_seqlens), derived from the prefix mask at the first run after an upload. Only valid rows are
+ * computed; per-row outputs (token heads) are scattered back to the plan's b * L + i layout on read.
+ * One HIP stream per plan; a context is single-threaded by contract (one call in flight per plan,
+ * as src/encoder.ts:5-8 and 265-269 guarantee on the reference side).
+ */
+#ifndef KH_HIP_H
+#define KH_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct kh_ctx kh_ctx;
+typedef struct kh_plan kh_plan;
+
+/* status codes */
+#define KH_OK 0
+#define KH_EINVAL 1        /* bad argument, malformed plan JSON, size mismatch */
+#define KH_EUNSUPPORTED 2  /* a plan op or layout this executor does not run */
+#define KH_EHIP 3          /* a HIP runtime call failed (message names it) */
+#define KH_ENOMEM 4        /* device or host allocation failed */
+#define KH_ELOST 5         /* an earlier device failure latched the context; every call fails */
+
+/* tensor dtypes */
+#define KH_F32 0
+#define KH_F16 1
+#define KH_U32 2
+
+#define KH_ABI_VERSION 1
+
+/* Message of the calling thread's last failure ("" when none). Valid until the next call on the
+ * same thread. */
+const char *kh_last_error(void);
+int kh_abi_version(void);
+
+/* Context on HIP device `device`; owns the device copies of the weights.
+ * Replaces the weight upload of loadGpu (src/webgpu-backend.ts:53-101) / the WASM host's
+ * addWeight (src/plan/wasm.ts:231-255). */
+int kh_ctx_create(int device, kh_ctx **out);
+int kh_ctx_destroy(kh_ctx *ctx);
+
+/* One manifest tensor (name, dtype, row-major shape, bytes): copied to device memory before the
+ * call returns. A name loaded twice is an error (src/plan/wasm.ts:233). */
+int kh_weight_add(kh_ctx *ctx, const char *name, int dtype, const int64_t *shape, int ndim,
+                  const void *data, size_t bytes);
+
+/* Bytes of the loaded weights in device memory (Backend.weightBytes, src/backend.ts:92-93). */
+int kh_ctx_weight_bytes(const kh_ctx *ctx, uint64_t *out);
+
+/* Optional device-resident word table [rows, width] in `dtype` (the step before the plan: the
+ * reference gathers word rows on the host, src/encoder.ts:271-282); enables kh_upload_ids. */
+int kh_words_set(kh_ctx *ctx, int dtype, int64_t rows, int64_t width, const void *data, size_t bytes);
+
+/* Backend.check (src/backend.ts:94-95): KH_OK when the plan (JSON of the reference's Plan, typed
+ * `init` tables left out) can run here, else an error naming every op that cannot. With a null
+ * context only the plan's structure is checked (no weights, no device needed). */
+int kh_plan_check(kh_ctx *ctx, const char *plan_json, size_t len);
+
+/* Backend.runner (src/backend.ts:96, src/plan/executor.ts:85-99): builds every buffer and the
+ * launch list up front. */
+int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out);
+
+/* BufferDecl.init of buffer `id` (relidx, cossin, first, zero; src/plan/executor.ts:118-124). */
+int kh_plan_init_buffer(kh_plan *plan, const char *id, const void *data, size_t bytes);
+
+typedef struct {
+  int32_t length;       /* PlanRunner.length */
+  int32_t batch;        /* PlanRunner.batch */
+  int32_t markers;      /* PlanRunner.markers */
+  int32_t f16;          /* storage dtype of the plan */
+  uint64_t bytes;       /* PlanRunner.bytes: device bytes held for this plan */
+  int32_t out_rows;     /* Plan.output.rows */
+  int32_t out_cols;     /* Plan.output.cols */
+  int32_t launches;     /* kernel launches of one run */
+  int32_t reserved;
+} kh_plan_info;
+
+int kh_plan_info_get(const kh_plan *plan, kh_plan_info *out);
+
+/* PlanRunner.upload (src/plan/executor.ts:365-393): word rows [L * B, E] in the plan's storage
+ * dtype, the f32 mask [L * B] and, for plans with a typeIds input, u32 type ids [L * B] (position
+ * row in the high 16 bits for POSIDS). Copied before return; the mask must be a prefix mask of
+ * 0/1 per sequence (as every reference engine fills it, src/wasm/plan.ts:13-14). */
+int kh_upload(kh_plan *plan, const void *emb, size_t emb_bytes, const float *mask, size_t mask_count,
+              const uint32_t *type_ids, size_t type_count);
+
+/* Variant of kh_upload with token ids [L * B] instead of word rows: the rows are gathered from
+ * the context's word table (kh_words_set) on the device. */
+int kh_upload_ids(kh_plan *plan, const int32_t *ids, size_t id_count, const float *mask,
+                  size_t mask_count, const uint32_t *type_ids, size_t type_count);
+
+/* PlanRunner.run (src/plan/executor.ts:294-297): one forward over `rows` rows (the real rows of
+ * a B = 1 call, L * B for a batch plan), enqueued on the plan's stream; returns without waiting. */
+int kh_run(kh_plan *plan, int32_t rows);
+
+/* PlanRunner.readOutput (src/plan/executor.ts:395-408): waits, then writes rows * cols f32
+ * values (f16 storage converted) in the plan's output layout. */
+int kh_read_output(kh_plan *plan, float *out, size_t count);
+
+/* Waits for the plan's stream. */
+int kh_sync(kh_plan *plan);
+
+/* GPU milliseconds of the last kh_run (hipEvents on the plan's stream around its launches). */
+int kh_last_run_ms(kh_plan *plan, float *ms);
+
+/* Per-launch profile: runs one forward with an event pair around every launch and fills up to
+ * `cap` records (name of the op, kernel, GPU ms, algorithmic FLOPs and bytes of that launch).
+ * Returns the number of launches in *count. */
+typedef struct {
+  char name[48];
+  char kernel[24];
+  float ms;
+  float reserved;
+  double flops;
+  double bytes;
+} kh_launch_stat;
+
+int kh_profile(kh_plan *plan, int32_t rows, kh_launch_stat *out, int32_t cap, int32_t *count);
+
+/* Packed rows (sum of valid sequence lengths) of the last run. */
+int kh_packed_rows(const kh_plan *plan, int64_t *out);
+
+int kh_plan_destroy(kh_plan *plan);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KH_HIP_H */

@@ -1,0 +1,260 @@
+"""HIP backend over the C ABI of libkh_hip.so (include/kh_hip.h).
+
+`HipBackend` and `HipPlanRunner` mirror the reference's Backend / PlanRunner seam
+(src/backend.ts:14-46) method for method, so the parity tests and the benchmark drive the HIP
+executor the way EncoderModel drives the WebGPU or WASM executors. There is no fallback: if the
+library is missing or a call fails, the error surfaces (a GPU run never silently computes on the
+CPU).
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+
+import numpy as np
+
+from .plan.build import plan_inits, plan_json
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkh_hip.so")
+
+KH_F32, KH_F16, KH_U32 = 0, 1, 2
+ERRORS = {1: "EINVAL", 2: "EUNSUPPORTED", 3: "EHIP", 4: "ENOMEM", 5: "ELOST"}
+
+# every entry point declared in include/kh_hip.h
+EXPORTS = [
+    "kh_last_error", "kh_abi_version", "kh_ctx_create", "kh_ctx_destroy", "kh_weight_add",
+    "kh_ctx_weight_bytes", "kh_words_set", "kh_plan_check", "kh_plan_create", "kh_plan_init_buffer",
+    "kh_plan_info_get", "kh_upload", "kh_upload_ids", "kh_run", "kh_read_output", "kh_sync",
+    "kh_last_run_ms", "kh_profile", "kh_packed_rows", "kh_plan_destroy",
+]
+
+
+class KhError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"kh {ERRORS.get(code, code)}: {message}")
+        self.code = code
+
+
+class PlanInfo(ctypes.Structure):
+    _fields_ = [("length", ctypes.c_int32), ("batch", ctypes.c_int32), ("markers", ctypes.c_int32),
+                ("f16", ctypes.c_int32), ("bytes", ctypes.c_uint64), ("out_rows", ctypes.c_int32),
+                ("out_cols", ctypes.c_int32), ("launches", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+class LaunchStat(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 48), ("kernel", ctypes.c_char * 24), ("ms", ctypes.c_float),
+                ("reserved", ctypes.c_float), ("flops", ctypes.c_double), ("bytes", ctypes.c_double)]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The in-tree libkh_hip.so; raises when it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built (python -m kleinhirn_amd.build)")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, sz, i32, i64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_int64
+    L.kh_last_error.restype = ctypes.c_char_p
+    L.kh_last_error.argtypes = []
+    L.kh_abi_version.restype = ctypes.c_int
+    sigs = {
+        "kh_ctx_create": [ctypes.c_int, ctypes.POINTER(vp)],
+        "kh_ctx_destroy": [vp],
+        "kh_weight_add": [vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(i64), ctypes.c_int, vp, sz],
+        "kh_ctx_weight_bytes": [vp, ctypes.POINTER(ctypes.c_uint64)],
+        "kh_words_set": [vp, ctypes.c_int, i64, i64, vp, sz],
+        "kh_plan_check": [vp, ctypes.c_char_p, sz],
+        "kh_plan_create": [vp, ctypes.c_char_p, sz, ctypes.POINTER(vp)],
+        "kh_plan_init_buffer": [vp, ctypes.c_char_p, vp, sz],
+        "kh_plan_info_get": [vp, ctypes.POINTER(PlanInfo)],
+        "kh_upload": [vp, vp, sz, vp, sz, vp, sz],
+        "kh_upload_ids": [vp, vp, sz, vp, sz, vp, sz],
+        "kh_run": [vp, i32],
+        "kh_read_output": [vp, vp, sz],
+        "kh_sync": [vp],
+        "kh_last_run_ms": [vp, ctypes.POINTER(ctypes.c_float)],
+        "kh_profile": [vp, i32, ctypes.POINTER(LaunchStat), i32, ctypes.POINTER(i32)],
+        "kh_packed_rows": [vp, ctypes.POINTER(i64)],
+        "kh_plan_destroy": [vp],
+    }
+    for name, args in sigs.items():
+        fn = getattr(L, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise KhError(rc, lib().kh_last_error().decode("utf-8", "replace"))
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else ctypes.c_void_p(a.ctypes.data)
+
+
+class HipPlanRunner:
+    """PlanRunner (src/backend.ts:14-28) of one plan on the HIP device."""
+
+    def __init__(self, backend: "HipBackend", plan: dict):
+        self.backend = backend
+        self.plan = plan
+        doc = json.dumps(plan_json(plan)).encode("utf-8")
+        h = ctypes.c_void_p()
+        _check(lib().kh_plan_create(backend.ctx, doc, len(doc), ctypes.byref(h)))
+        self.h = h
+        for bid, raw in plan_inits(plan).items():
+            buf = np.frombuffer(raw, dtype=np.uint8)
+            _check(lib().kh_plan_init_buffer(self.h, bid.encode(), _ptr(buf), buf.nbytes))
+        self.length = plan["length"]
+        self.batch = plan["batch"]
+        self.markers = plan["markers"]
+        self._keep = None
+
+    @property
+    def info(self) -> PlanInfo:
+        info = PlanInfo()
+        _check(lib().kh_plan_info_get(self.h, ctypes.byref(info)))
+        return info
+
+    @property
+    def bytes(self) -> int:
+        return int(self.info.bytes)
+
+    def upload(self, inp: dict) -> None:
+        """RunInput {embeddings, mask, typeIds?} (src/plan/executor.ts:25-32)."""
+        emb = np.ascontiguousarray(inp["embeddings"])
+        want = np.float16 if self.plan["f16"] else np.float32
+        if emb.dtype != want:
+            raise TypeError(f"word rows must be {np.dtype(want).name} for this plan")
+        mask = np.ascontiguousarray(inp["mask"], dtype=np.float32)
+        tt = inp.get("typeIds")
+        tt = None if tt is None else np.ascontiguousarray(tt, dtype=np.uint32)
+        _check(lib().kh_upload(self.h, _ptr(emb), emb.nbytes, _ptr(mask), mask.size, _ptr(tt),
+                               0 if tt is None else tt.size))
+
+    def upload_ids(self, ids: np.ndarray, mask: np.ndarray, type_ids: np.ndarray | None = None) -> None:
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        mask = np.ascontiguousarray(mask, dtype=np.float32)
+        tt = None if type_ids is None else np.ascontiguousarray(type_ids, dtype=np.uint32)
+        _check(lib().kh_upload_ids(self.h, _ptr(ids), ids.size, _ptr(mask), mask.size, _ptr(tt),
+                                   0 if tt is None else tt.size))
+
+    def run(self, seq_len: int, capture: bool = False) -> None:
+        if capture:
+            raise RuntimeError("capture is a WebGPU parity tool; the HIP runner has no capture")
+        _check(lib().kh_run(self.h, int(seq_len)))
+
+    def sync(self) -> None:
+        _check(lib().kh_sync(self.h))
+
+    def read_output(self) -> np.ndarray:
+        o = self.plan["output"]
+        out = np.empty(o["rows"] * o["cols"], dtype=np.float32)
+        _check(lib().kh_read_output(self.h, _ptr(out), out.size))
+        return out
+
+    def read_capture(self):
+        raise RuntimeError("capture is a WebGPU parity tool; the HIP runner has no capture")
+
+    def assert_capturable(self) -> None:
+        raise RuntimeError("capture is a WebGPU parity tool; the HIP runner has no capture")
+
+    def last_run_ms(self) -> float:
+        ms = ctypes.c_float()
+        _check(lib().kh_last_run_ms(self.h, ctypes.byref(ms)))
+        return float(ms.value)
+
+    def packed_rows(self) -> int:
+        n = ctypes.c_int64()
+        _check(lib().kh_packed_rows(self.h, ctypes.byref(n)))
+        return int(n.value)
+
+    def profile(self, rows: int) -> list[dict]:
+        cap = 4096
+        arr = (LaunchStat * cap)()
+        n = ctypes.c_int32()
+        _check(lib().kh_profile(self.h, int(rows), arr, cap, ctypes.byref(n)))
+        return [{"name": arr[i].name.decode(), "kernel": arr[i].kernel.decode(), "ms": float(arr[i].ms),
+                 "flops": float(arr[i].flops), "bytes": float(arr[i].bytes)} for i in range(min(n.value, cap))]
+
+    def destroy(self) -> None:
+        if self.h:
+            _check(lib().kh_plan_destroy(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class HipBackend:
+    """Backend (src/backend.ts:30-46) on one HIP device."""
+
+    kind = "hip"
+
+    def __init__(self, weights: dict[str, np.ndarray], device: int = 0):
+        h = ctypes.c_void_p()
+        _check(lib().kh_ctx_create(int(device), ctypes.byref(h)))
+        self.ctx = h
+        self.device = device
+        for name, t in weights.items():
+            self.add_weight(name, t)
+
+    def add_weight(self, name: str, t: np.ndarray) -> None:
+        t = np.ascontiguousarray(t)
+        dtype = {np.dtype(np.float32): KH_F32, np.dtype(np.float16): KH_F16, np.dtype(np.uint32): KH_U32}[t.dtype]
+        shape = (ctypes.c_int64 * max(1, t.ndim))(*t.shape)
+        _check(lib().kh_weight_add(self.ctx, name.encode(), dtype, shape, t.ndim, _ptr(t), t.nbytes))
+
+    def set_words(self, table: np.ndarray) -> None:
+        """Device-resident word table for runs by token id (upload_ids)."""
+        t = np.ascontiguousarray(table)
+        dtype = KH_F16 if t.dtype == np.float16 else KH_F32
+        _check(lib().kh_words_set(self.ctx, dtype, t.shape[0], t.shape[1], _ptr(t), t.nbytes))
+
+    @property
+    def weight_bytes(self) -> int:
+        v = ctypes.c_uint64()
+        _check(lib().kh_ctx_weight_bytes(self.ctx, ctypes.byref(v)))
+        return int(v.value)
+
+    def check(self, plan: dict) -> None:
+        doc = json.dumps(plan_json(plan)).encode("utf-8")
+        _check(lib().kh_plan_check(self.ctx, doc, len(doc)))
+
+    def runner(self, plan: dict) -> HipPlanRunner:
+        return HipPlanRunner(self, plan)
+
+    def fit_batch(self, build, batch: int):
+        """One packed plan holds any batch that fits the device: the largest asked size."""
+        return build(batch)
+
+    def prepare(self, work):
+        return work()
+
+    def call(self, start, read):
+        return read(start())
+
+    def info(self) -> dict:
+        return {"backend": "hip", "device": self.device, "weightBytes": self.weight_bytes}
+
+    def dispose(self) -> None:
+        if self.ctx:
+            _check(lib().kh_ctx_destroy(self.ctx))
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.dispose()
+        except Exception:
+            pass

@@ -1,0 +1,102 @@
+// Launch interface of the gfx950 kernels. Every launch is asynchronous on the given stream;
+// operand shapes are checked by the caller (runner.hip) before a launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace kh {
+
+// Activation codes of the plan's matmul ACT constant (src/plan/build.ts:91).
+enum Act : int { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2, ACT_TANH = 3, ACT_SILU = 4 };
+
+// C[M, N] = act(A[M, K] W[N, K]^T + bias[N]); row strides lda, ldw, ldc in elements.
+struct GemmArgs {
+  const void *a;
+  int64_t lda;
+  const void *w;
+  int64_t ldw;
+  const void *bias;  // may be null
+  void *c;
+  int64_t ldc;
+  int M, N, K;
+  int act;
+  // batched over z: pointer offsets (elements) per z index
+  int batch = 1;
+  int64_t a_bs = 0, w_bs = 0, c_bs = 0;
+  bool c_f32 = false;  // write f32 output whatever the storage type (relative-position scores)
+  // one wavefront per output group: pooled-head steps, so a sequence's result does not depend on
+  // how many sequences share the batch
+  bool rowdot = false;
+};
+void gemm(bool f16, const GemmArgs &g, hipStream_t s);
+// true when the MFMA tile kernel runs this shape (else the wave-per-output kernel)
+bool gemm_uses_mfma(bool f16, const GemmArgs &g);
+
+// Packed-row description of one run: cu[b] .. cu[b+1] are the rows of sequence b.
+struct Packing {
+  const int32_t *cu;       // [B + 1]
+  const int32_t *row_pos;  // [T] position of the row inside its sequence
+  const int32_t *row_seq;  // [T] sequence of the row
+  int32_t B;
+  int64_t T;
+};
+
+struct EmbLnArgs {
+  const void *word;        // packed word rows [T, N], or null with table + ids
+  const void *table;       // device word table [rows, N]
+  const int32_t *ids;      // packed ids [T]
+  const void *pos;         // [maxpos, N] or null (zero table)
+  const void *typ;         // [types, N] or null (zero table)
+  const uint32_t *tt;      // packed type ids [T] or null
+  const void *gamma, *beta;
+  void *out;
+  int N, offset, maxpos, posids;
+  float eps;
+};
+void embln(bool f16, const EmbLnArgs &a, const Packing &p, hipStream_t s);
+
+// LN over rows: MODE 2 adds b first. rows = T (packed) or B (sequence rows).
+void layernorm(bool f16, const void *a, const void *b, const void *gamma, const void *beta, void *out,
+               int64_t rows, int N, float eps, hipStream_t s);
+
+// dst += src (MODE 0) or dst[r] += src[seq(r)] (MODE 1), rounded to storage.
+void add(bool f16, void *dst, const void *src, int64_t rows, int N, int mode, const Packing &p,
+         hipStream_t s);
+
+void geglu(bool f16, const void *mid, void *gate, int64_t rows, int I, hipStream_t s);
+
+void rope(bool f16, void *qkv, const float *cossin, int64_t rows, int H, int D, int L,
+          const Packing &p, hipStream_t s);
+
+// mode 0 mean, 1 max over the packed rows of each sequence -> [B, N]
+void pool(bool f16, const void *x, void *out, int N, int mode, const Packing &p, hipStream_t s);
+
+// states[b K + k] = x[cu[b] + marker[b 3 K + k]] (zero row when the marker is past the sequence)
+void gather_rows(bool f16, const void *x, const uint32_t *markers, void *states, int K, int D,
+                 const Packing &p, hipStream_t s);
+
+// Standard attention over packed rows: ctx = softmax(scale q k^T, window) v per (sequence, head).
+// tiles: [ntiles] (sequence, first query) pairs of 64-query tiles.
+struct AttnArgs {
+  const void *qkv;   // [T, 3 H D]
+  void *ctx;         // [T, H D]
+  int H, D;
+  float scale;       // multiplies q.k (standard) ...
+  int window;        // 0: global, else |i - j| <= window
+  // DeBERTa relative terms: score = (q.k + c2p[i][h][bucket] + p2c[j][h][bucket]) * scale
+  const float *c2p = nullptr;  // [T, H, NB]
+  const float *p2c = nullptr;  // [T, H, NB]
+  const int32_t *bucket = nullptr;  // [2 Lmax - 1] bucket of (i - j) + Lmax - 1
+  int nb = 0;
+  int lmax = 0;
+  const int2 *tiles;
+  int ntiles;
+};
+void attention(bool f16, const AttnArgs &a, const Packing &p, hipStream_t s);
+constexpr int ATTN_QTILE = 64;
+
+// Convert storage rows to f32 (readback of f16 outputs).
+void to_f32(bool f16, const void *src, float *dst, int64_t n, hipStream_t s);
+
+}  // namespace kh

@@ -1,0 +1,388 @@
+// Bandwidth-bound row kernels over packed rows: embedding gather + LayerNorm, LayerNorm with the
+// residual fused, residual add, GeGLU, RoPE, pooling, row gather, f16 -> f32 readback.
+// One 64-lane wavefront per row for the normalisations: the row stays in registers between the
+// mean and the variance pass (variance = mean((v - mean)^2), the reference's two-pass form,
+// src/wasm/plan.ts:386-411), loads are VEC-wide and coalesced across the wavefront.
+#include "kernels.h"
+#include "device.h"
+
+namespace kh {
+
+namespace {
+
+constexpr int ROWS_PER_BLOCK = 4;  // wavefronts (rows) per 256-thread block
+
+// Per lane: PER groups of VEC contiguous elements; group g = k * 64 + lane.
+template <typename T, int VEC, int PER>
+__device__ __forceinline__ void ln_finish(float (&v)[PER][VEC], int N, const T *gamma, const T *beta,
+                                          float eps, T *out, int lane) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    int e0 = (k * WAVE + lane) * VEC;
+#pragma unroll
+    for (int i = 0; i < VEC; i++) s += (e0 + i < N) ? v[k][i] : 0.f;
+  }
+  float mean = wave_sum(s) / (float)N;
+  float sq = 0.f;
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    int e0 = (k * WAVE + lane) * VEC;
+#pragma unroll
+    for (int i = 0; i < VEC; i++) {
+      float d = v[k][i] - mean;
+      sq += (e0 + i < N) ? d * d : 0.f;
+    }
+  }
+  float var = wave_sum(sq) / (float)N;
+  float inv = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    int e0 = (k * WAVE + lane) * VEC;
+    if (e0 >= N) continue;
+    float g[VEC], b[VEC], y[VEC];
+    VecIO<T, VEC>::load(gamma + e0, g);
+    if (beta) VecIO<T, VEC>::load(beta + e0, b);
+#pragma unroll
+    for (int i = 0; i < VEC; i++) y[i] = (v[k][i] - mean) * inv * g[i] + (beta ? b[i] : 0.f);
+    VecIO<T, VEC>::store(out + e0, y);
+  }
+}
+
+template <typename T, int VEC, int PER>
+__global__ void __launch_bounds__(256) layernorm_kernel(const T *__restrict__ a, const T *__restrict__ b,
+                                                        const T *__restrict__ gamma, const T *__restrict__ beta,
+                                                        T *__restrict__ out, int64_t rows, int N, float eps) {
+  int lane = threadIdx.x & 63;
+  int64_t r = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const T *ar = a + r * N;
+  const T *br = b ? b + r * N : nullptr;
+  float v[PER][VEC];
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    int e0 = (k * WAVE + lane) * VEC;
+    if (e0 < N) {
+      VecIO<T, VEC>::load(ar + e0, v[k]);
+      if (br) {
+        float y[VEC];
+        VecIO<T, VEC>::load(br + e0, y);
+#pragma unroll
+        for (int i = 0; i < VEC; i++) v[k][i] += y[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; i++) v[k][i] = 0.f;
+    }
+  }
+  ln_finish<T, VEC, PER>(v, N, gamma, beta, eps, out + r * N, lane);
+}
+
+// word + position + type in f32 ((word + pos) + type), then LayerNorm (src/wasm/plan.ts:433-447).
+// Position row: tt >> 16 with POSIDS, else the row's position in its sequence + OFFSET, clamped to
+// MAXPOS - 1. Type row: tt & 0xffff.
+template <typename T, int VEC, int PER>
+__global__ void __launch_bounds__(256) embln_kernel(EmbLnArgs a, Packing p) {
+  int lane = threadIdx.x & 63;
+  int64_t r = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
+  if (r >= p.T) return;
+  const int N = a.N;
+  uint32_t t = a.tt ? a.tt[r] : 0u;
+  int prow = a.posids ? (int)(t >> 16) : p.row_pos[r] + a.offset;
+  prow = prow < a.maxpos - 1 ? prow : a.maxpos - 1;
+  const T *word = a.word ? (const T *)a.word + r * N : (const T *)a.table + (int64_t)a.ids[r] * N;
+  const T *pos = a.pos ? (const T *)a.pos + (int64_t)prow * N : nullptr;
+  const T *typ = a.typ ? (const T *)a.typ + (int64_t)(t & 0xffffu) * N : nullptr;
+  float v[PER][VEC];
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    int e0 = (k * WAVE + lane) * VEC;
+    if (e0 < N) {
+      float w[VEC], q[VEC], y[VEC];
+      VecIO<T, VEC>::load(word + e0, w);
+      if (pos) VecIO<T, VEC>::load(pos + e0, q);
+      if (typ) VecIO<T, VEC>::load(typ + e0, y);
+#pragma unroll
+      for (int i = 0; i < VEC; i++) v[k][i] = (w[i] + (pos ? q[i] : 0.f)) + (typ ? y[i] : 0.f);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; i++) v[k][i] = 0.f;
+    }
+  }
+  ln_finish<T, VEC, PER>(v, N, (const T *)a.gamma, (const T *)a.beta, a.eps, (T *)a.out + r * N, lane);
+}
+
+template <typename T, int VEC>
+int pick_per(int N) {
+  return (N + WAVE * VEC - 1) / (WAVE * VEC);
+}
+
+template <typename T, int VEC, typename F>
+bool dispatch_per(int N, F &&f) {
+  int per = pick_per<T, VEC>(N);
+  switch (per) {
+    case 1: f(std::integral_constant<int, 1>()); return true;
+    case 2: f(std::integral_constant<int, 2>()); return true;
+    case 3: f(std::integral_constant<int, 3>()); return true;
+    case 4: f(std::integral_constant<int, 4>()); return true;
+    case 5: f(std::integral_constant<int, 5>()); return true;
+    case 6: f(std::integral_constant<int, 6>()); return true;
+    case 8: f(std::integral_constant<int, 8>()); return true;
+    default:
+      if (per <= 8) { f(std::integral_constant<int, 8>()); return true; }
+      if (per <= 12) { f(std::integral_constant<int, 12>()); return true; }
+      if (per <= 16) { f(std::integral_constant<int, 16>()); return true; }
+      return false;
+  }
+}
+
+template <typename T>
+void layernorm_t(const void *a, const void *b, const void *gamma, const void *beta, void *out, int64_t rows,
+                 int N, float eps, hipStream_t s) {
+  dim3 grid((unsigned)((rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK));
+  auto go = [&](auto vec) {
+    constexpr int VEC = decltype(vec)::value;
+    dispatch_per<T, VEC>(N, [&](auto per) {
+      constexpr int PER = decltype(per)::value;
+      hipLaunchKernelGGL((layernorm_kernel<T, VEC, PER>), grid, dim3(256), 0, s, (const T *)a, (const T *)b,
+                         (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps);
+    });
+  };
+  if (N % 4 == 0) go(std::integral_constant<int, 4>());
+  else if (N % 2 == 0) go(std::integral_constant<int, 2>());
+  else go(std::integral_constant<int, 1>());
+}
+
+template <typename T>
+void embln_t(const EmbLnArgs &a, const Packing &p, hipStream_t s) {
+  dim3 grid((unsigned)((p.T + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK));
+  auto go = [&](auto vec) {
+    constexpr int VEC = decltype(vec)::value;
+    dispatch_per<T, VEC>(a.N, [&](auto per) {
+      constexpr int PER = decltype(per)::value;
+      hipLaunchKernelGGL((embln_kernel<T, VEC, PER>), grid, dim3(256), 0, s, a, p);
+    });
+  };
+  if (a.N % 4 == 0) go(std::integral_constant<int, 4>());
+  else if (a.N % 2 == 0) go(std::integral_constant<int, 2>());
+  else go(std::integral_constant<int, 1>());
+}
+
+// dst += src in f32, rounded to storage (src/plan/layers.ts:496-498); MODE 1 adds the row of the
+// row's sequence.
+template <typename T>
+__global__ void __launch_bounds__(256) add_kernel(T *__restrict__ dst, const T *__restrict__ src, int64_t total,
+                                                  int N, int mode, const int32_t *__restrict__ row_seq) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    float s = mode == 0 ? (float)src[i] : (float)src[(int64_t)row_seq[i / N] * N + i % N];
+    dst[i] = (T)((float)dst[i] + s);
+  }
+}
+
+template <typename VT, typename T, int VEC>
+__global__ void __launch_bounds__(256) add_vec_kernel(T *__restrict__ dst, const T *__restrict__ src, int64_t nvec) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nvec; i += stride) {
+    float x[VEC], y[VEC];
+    VecIO<T, VEC>::load(dst + i * VEC, x);
+    VecIO<T, VEC>::load(src + i * VEC, y);
+#pragma unroll
+    for (int k = 0; k < VEC; k++) x[k] += y[k];
+    VecIO<T, VEC>::store(dst + i * VEC, x);
+  }
+}
+
+// gate[r, j] = gelu(mid[r, j]) mid[r, I + j] (src/wasm/plan.ts:500-508)
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256) geglu_kernel(const T *__restrict__ mid, T *__restrict__ gate, int64_t rows,
+                                                    int I) {
+  int64_t per_row = I / VEC;
+  int64_t total = rows * per_row;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    int64_t r = i / per_row;
+    int64_t j = (i - r * per_row) * VEC;
+    float x[VEC], y[VEC], o[VEC];
+    VecIO<T, VEC>::load(mid + r * 2 * I + j, x);
+    VecIO<T, VEC>::load(mid + r * 2 * I + I + j, y);
+#pragma unroll
+    for (int k = 0; k < VEC; k++) o[k] = gelu_as(x[k]) * y[k];
+    VecIO<T, VEC>::store(gate + r * I + j, o);
+  }
+}
+
+// rotate-half RoPE on q and k of head h, table row = position of the row in its sequence
+// (src/wasm/plan.ts:510-528)
+template <typename T>
+__global__ void __launch_bounds__(256) rope_kernel(T *__restrict__ qkv, const float *__restrict__ cossin,
+                                                   int64_t rows, int H, int D, const int32_t *__restrict__ row_pos) {
+  int half = D / 2;
+  int64_t per_row = (int64_t)2 * H * half;
+  int64_t total = rows * per_row;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    int64_t r = i / per_row;
+    int rem = (int)(i - r * per_row);
+    int sidx = rem / half, d = rem - sidx * half;
+    T *base = qkv + r * 3 * H * D + (int64_t)sidx * D;
+    const float *t = cossin + (int64_t)row_pos[r] * 2 * D;
+    float x = (float)base[d], y = (float)base[d + half], c = t[d], sn = t[D + d];
+    base[d] = (T)(x * c - y * sn);
+    base[d + half] = (T)(y * c + x * sn);
+  }
+}
+
+// masked mean (count floor 1e-9) or max per sequence and column (src/wasm/plan.ts:474-498); the
+// valid rows of a packed sequence are all its rows.
+template <typename T>
+__global__ void __launch_bounds__(64) pool_kernel(const T *__restrict__ x, T *__restrict__ out, int N, int mode,
+                                                  const int32_t *__restrict__ cu) {
+  int b = blockIdx.y;
+  int d = blockIdx.x * 64 + threadIdx.x;
+  if (d >= N) return;
+  int r0 = cu[b], r1 = cu[b + 1];
+  float acc = 0.f;
+  if (mode == 0) {
+    float cnt = 0.f;
+    for (int r = r0; r < r1; r++) {
+      acc += (float)x[(int64_t)r * N + d];
+      cnt += 1.f;
+    }
+    out[(int64_t)b * N + d] = (T)(acc / fmaxf(cnt, 1e-9f));
+  } else {
+    bool found = false;
+    for (int r = r0; r < r1; r++) {
+      float v = (float)x[(int64_t)r * N + d];
+      acc = found ? fmaxf(acc, v) : v;
+      found = true;
+    }
+    out[(int64_t)b * N + d] = (T)acc;
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) gather_kernel(const T *__restrict__ x, const uint32_t *__restrict__ markers,
+                                                     T *__restrict__ states, int K, int D, int B,
+                                                     const int32_t *__restrict__ cu) {
+  int64_t total = (int64_t)B * K * D;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    int64_t g = i / D;
+    int d = (int)(i - g * D);
+    int b = (int)(g / K);
+    uint32_t m = markers ? markers[(int64_t)b * 3 * K + (g - (int64_t)b * K)] : 0u;
+    int n = cu[b + 1] - cu[b];
+    states[i] = (int64_t)m < n ? x[((int64_t)cu[b] + m) * D + d] : (T)0.f;
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) to_f32_kernel(const T *__restrict__ src, float *__restrict__ dst, int64_t n) {
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = (float)src[i];
+}
+
+unsigned grid_for(int64_t n, int per_thread = 1) {
+  int64_t blocks = (n / per_thread + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 65536) blocks = 65536;
+  return (unsigned)blocks;
+}
+
+}  // namespace
+
+void layernorm(bool f16, const void *a, const void *b, const void *gamma, const void *beta, void *out,
+               int64_t rows, int N, float eps, hipStream_t s) {
+  if (rows <= 0) return;
+  if (f16) layernorm_t<half_t>(a, b, gamma, beta, out, rows, N, eps, s);
+  else layernorm_t<float>(a, b, gamma, beta, out, rows, N, eps, s);
+}
+
+void embln(bool f16, const EmbLnArgs &a, const Packing &p, hipStream_t s) {
+  if (p.T <= 0) return;
+  if (f16) embln_t<half_t>(a, p, s);
+  else embln_t<float>(a, p, s);
+}
+
+void add(bool f16, void *dst, const void *src, int64_t rows, int N, int mode, const Packing &p, hipStream_t s) {
+  int64_t total = rows * N;
+  if (total <= 0) return;
+  if (mode == 0 && f16 && total % 8 == 0) {
+    hipLaunchKernelGGL((add_vec_kernel<half8v, half_t, 8>), dim3(grid_for(total / 8)), dim3(256), 0, s,
+                       (half_t *)dst, (const half_t *)src, total / 8);
+  } else if (mode == 0 && !f16 && total % 4 == 0) {
+    hipLaunchKernelGGL((add_vec_kernel<float4v, float, 4>), dim3(grid_for(total / 4)), dim3(256), 0, s,
+                       (float *)dst, (const float *)src, total / 4);
+  } else if (f16) {
+    hipLaunchKernelGGL((add_kernel<half_t>), dim3(grid_for(total)), dim3(256), 0, s, (half_t *)dst,
+                       (const half_t *)src, total, N, mode, p.row_seq);
+  } else {
+    hipLaunchKernelGGL((add_kernel<float>), dim3(grid_for(total)), dim3(256), 0, s, (float *)dst,
+                       (const float *)src, total, N, mode, p.row_seq);
+  }
+}
+
+void geglu(bool f16, const void *mid, void *gate, int64_t rows, int I, hipStream_t s) {
+  if (rows <= 0) return;
+  if (f16) {
+    if (I % 8 == 0)
+      hipLaunchKernelGGL((geglu_kernel<half_t, 8>), dim3(grid_for(rows * I / 8)), dim3(256), 0, s,
+                         (const half_t *)mid, (half_t *)gate, rows, I);
+    else
+      hipLaunchKernelGGL((geglu_kernel<half_t, 1>), dim3(grid_for(rows * I)), dim3(256), 0, s,
+                         (const half_t *)mid, (half_t *)gate, rows, I);
+  } else {
+    if (I % 4 == 0)
+      hipLaunchKernelGGL((geglu_kernel<float, 4>), dim3(grid_for(rows * I / 4)), dim3(256), 0, s,
+                         (const float *)mid, (float *)gate, rows, I);
+    else
+      hipLaunchKernelGGL((geglu_kernel<float, 1>), dim3(grid_for(rows * I)), dim3(256), 0, s,
+                         (const float *)mid, (float *)gate, rows, I);
+  }
+}
+
+void rope(bool f16, void *qkv, const float *cossin, int64_t rows, int H, int D, int L, const Packing &p,
+          hipStream_t s) {
+  (void)L;
+  int64_t total = rows * 2 * H * (D / 2);
+  if (total <= 0) return;
+  if (f16)
+    hipLaunchKernelGGL((rope_kernel<half_t>), dim3(grid_for(total)), dim3(256), 0, s, (half_t *)qkv, cossin,
+                       rows, H, D, p.row_pos);
+  else
+    hipLaunchKernelGGL((rope_kernel<float>), dim3(grid_for(total)), dim3(256), 0, s, (float *)qkv, cossin, rows,
+                       H, D, p.row_pos);
+}
+
+void pool(bool f16, const void *x, void *out, int N, int mode, const Packing &p, hipStream_t s) {
+  if (p.B <= 0) return;
+  dim3 grid((unsigned)((N + 63) / 64), (unsigned)p.B);
+  if (f16)
+    hipLaunchKernelGGL((pool_kernel<half_t>), grid, dim3(64), 0, s, (const half_t *)x, (half_t *)out, N, mode,
+                       p.cu);
+  else
+    hipLaunchKernelGGL((pool_kernel<float>), grid, dim3(64), 0, s, (const float *)x, (float *)out, N, mode, p.cu);
+}
+
+void gather_rows(bool f16, const void *x, const uint32_t *markers, void *states, int K, int D, const Packing &p,
+                 hipStream_t s) {
+  int64_t total = (int64_t)p.B * K * D;
+  if (total <= 0) return;
+  if (f16)
+    hipLaunchKernelGGL((gather_kernel<half_t>), dim3(grid_for(total)), dim3(256), 0, s, (const half_t *)x, markers,
+                       (half_t *)states, K, D, p.B, p.cu);
+  else
+    hipLaunchKernelGGL((gather_kernel<float>), dim3(grid_for(total)), dim3(256), 0, s, (const float *)x, markers,
+                       (float *)states, K, D, p.B, p.cu);
+}
+
+void to_f32(bool f16, const void *src, float *dst, int64_t n, hipStream_t s) {
+  if (n <= 0) return;
+  if (f16)
+    hipLaunchKernelGGL((to_f32_kernel<half_t>), dim3(grid_for(n)), dim3(256), 0, s, (const half_t *)src, dst, n);
+  else
+    hipLaunchKernelGGL((to_f32_kernel<float>), dim3(grid_for(n)), dim3(256), 0, s, (const float *)src, dst, n);
+}
+
+}  // namespace kh

@@ -1,0 +1,1272 @@
+// libkh_hip.so: the C ABI of include/kh_hip.h.
+//
+// A plan (the reference's Plan IR as JSON, src/plan/ir.ts:41-60) is lowered once at creation into
+// a list of launch steps over packed rows: the attention op sequences of the reference's split
+// kernels fuse into one flash-attention step (the same grouping the reference's WASM host makes,
+// src/plan/wasm.ts:53-82), the per-op row dispatch of the reference ('rows', 'rows16', ...) becomes
+// "all packed rows", and a fixed dispatch (pooled heads) becomes "one row per sequence". Buffers
+// no step reads after the fusion (scores, c2p, p2c, kinfo, mask) get no device memory.
+//
+// Per call the host hands padded RunInput arrays (src/plan/executor.ts:25-32); the first run after
+// an upload derives cu_seqlens from the prefix mask, packs the valid rows into pinned memory and
+// copies only those to the device.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <memory>
+#include <set>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/kh_hip.h"
+#include "json.h"
+#include "kernels.h"
+
+namespace kh {
+
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string &m) : std::runtime_error(m), code(c) {}
+};
+
+static thread_local std::string g_last_error;
+
+#define KH_CHECK(call)                                                                            \
+  do {                                                                                            \
+    hipError_t e_ = (call);                                                                       \
+    if (e_ != hipSuccess)                                                                         \
+      throw Error(KH_EHIP, std::string(#call) + ": " + hipGetErrorString(e_));                    \
+  } while (0)
+
+static void fail(int code, const std::string &m) { throw Error(code, m); }
+
+static size_t elem_size(int dtype) { return dtype == KH_F16 ? 2 : 4; }
+
+struct DevMem {
+  void *p = nullptr;
+  size_t bytes = 0;
+  DevMem() = default;
+  DevMem(const DevMem &) = delete;
+  DevMem &operator=(const DevMem &) = delete;
+  ~DevMem() { reset(); }
+  void alloc(size_t n) {
+    reset();
+    if (n == 0) n = 16;
+    hipError_t e = hipMalloc(&p, n);
+    if (e != hipSuccess) {
+      p = nullptr;
+      fail(KH_ENOMEM, "hipMalloc of " + std::to_string(n) + " bytes: " + hipGetErrorString(e));
+    }
+    bytes = n;
+  }
+  void reset() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+};
+
+struct HostPinned {
+  void *p = nullptr;
+  size_t bytes = 0;
+  ~HostPinned() { reset(); }
+  void ensure(size_t n) {
+    if (n <= bytes) return;
+    reset();
+    hipError_t e = hipHostMalloc(&p, n, hipHostMallocDefault);
+    if (e != hipSuccess) {
+      p = nullptr;
+      fail(KH_ENOMEM, "hipHostMalloc of " + std::to_string(n) + " bytes: " + hipGetErrorString(e));
+    }
+    bytes = n;
+  }
+  void reset() {
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+};
+
+struct Weight {
+  int dtype = KH_F32;
+  std::vector<int64_t> shape;
+  int64_t count = 0;
+  std::unique_ptr<DevMem> mem;
+};
+
+}  // namespace kh
+
+using namespace kh;
+
+struct kh_ctx {
+  int device = 0;
+  std::map<std::string, Weight> weights;
+  uint64_t weight_bytes = 0;
+  bool lost = false;
+  std::string lost_msg;
+  // device word table
+  int words_dtype = -1;
+  int64_t words_rows = 0, words_width = 0;
+  std::unique_ptr<DevMem> words;
+};
+
+namespace kh {
+
+enum StepKind { S_EMBLN, S_LN, S_GEMM, S_ADD, S_GEGLU, S_ROPE, S_ATTN, S_POOL, S_GATHER };
+
+// A buffer reference of a step: device pointer resolved at plan creation.
+struct Ref {
+  std::string id;
+  void *p = nullptr;
+};
+
+struct Step {
+  StepKind kind;
+  std::string name, kernel;
+  bool seq_rows = false;  // fixed dispatch: one row per sequence (or rows_fixed rows)
+  int64_t rows_fixed = 0;
+  Ref in[6];
+  int N = 0, K = 0, act = 0, mode = 0, I = 0, H = 0, D = 0, window = 0, offset = 0, maxpos = 1, posids = 0;
+  int Kmk = 1;  // gather markers per sequence
+  float eps = 0.f, scale = 1.f;
+  bool rel = false;
+  std::string markers_id;  // gather: the init buffer holding the markers
+};
+
+struct Buffer {
+  int64_t bytes = 0;
+  std::string usage;
+  bool used = false;
+  bool seq_space = false;  // written by a fixed-dispatch op: rows are sequences
+  bool packed_space = false;
+  std::unique_ptr<DevMem> mem;
+  std::vector<uint8_t> init;
+};
+
+static const std::set<std::string> kMatmul = {"matmul", "mmtile", "mmtile8", "mmtile16"};
+
+static bool is_rows_dim(const Json &d) { return d.kind == Json::Str; }
+
+}  // namespace kh
+
+struct kh_plan {
+  kh_ctx *ctx = nullptr;
+  bool f16 = false;
+  int L = 0, B = 0, markers = 0, E = 0;
+  std::map<std::string, Buffer> bufs;
+  std::vector<Step> steps;
+  std::string in_emb, in_mask, in_tt;
+  std::string out_buf;
+  int out_rows = 0, out_cols = 0;
+  bool out_packed = false;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  bool ran = false;
+
+  // upload staging (host, padded layout as the caller gave it)
+  std::vector<uint8_t> emb_host;
+  std::vector<float> mask_host;
+  std::vector<uint32_t> tt_host;
+  std::vector<int32_t> ids_host;
+  bool by_ids = false;
+  bool uploaded = false, dirty = true;
+  int last_rows = -1;
+
+  // packing of the current upload
+  std::vector<int32_t> cu;
+  int64_t T = 0;
+  int ntiles = 0;
+  double attn_pairs_global = 0;  // sum over sequences of n^2
+  std::map<int, double> attn_pairs_window;  // window -> sum of visited (i, j) pairs
+  HostPinned pin_emb, pin_meta;
+  DevMem d_cu, d_row_pos, d_row_seq, d_tiles, d_tt, d_ids;
+
+  // relative attention
+  std::vector<int32_t> bucket_host;
+  DevMem d_bucket;
+  DevMem d_c2p, d_p2c;
+  int rel_nb = 0;
+
+  // cos/sin tables (f32)
+  std::map<std::string, std::unique_ptr<DevMem>> tables;
+};
+
+namespace kh {
+
+static Packing packing_of(kh_plan *pl) {
+  Packing p;
+  p.cu = (const int32_t *)pl->d_cu.p;
+  p.row_pos = (const int32_t *)pl->d_row_pos.p;
+  p.row_seq = (const int32_t *)pl->d_row_seq.p;
+  p.B = pl->B;
+  p.T = pl->T;
+  return p;
+}
+
+// ---- plan parsing and lowering -------------------------------------------------------------
+
+struct Parsed {
+  Json root;
+  std::vector<Json> ops;  // flattened op list
+};
+
+static Parsed parse_plan(const char *json, size_t len) {
+  Parsed p;
+  if (!json || len == 0) fail(KH_EINVAL, "empty plan JSON");
+  try {
+    p.root = JsonReader(json, len).parse();
+  } catch (const std::runtime_error &e) {
+    fail(KH_EINVAL, e.what());
+  }
+  for (const Json &seg : p.root.at("segments").arr())
+    for (const Json &op : seg.at("ops").arr()) p.ops.push_back(op);
+  return p;
+}
+
+static int cint(const Json &op, const char *k) {
+  const Json &c = op.at("constants");
+  if (!c.has(k)) fail(KH_EINVAL, "op " + op.at("name").str() + ": constant " + k + " missing");
+  return (int)c.at(k).integer();
+}
+static double cnum(const Json &op, const char *k) {
+  const Json &c = op.at("constants");
+  if (!c.has(k)) fail(KH_EINVAL, "op " + op.at("name").str() + ": constant " + k + " missing");
+  return c.at(k).num();
+}
+static const std::string &bind(const Json &op, size_t i) {
+  const auto &b = op.at("bind").arr();
+  if (i >= b.size()) fail(KH_EINVAL, "op " + op.at("name").str() + ": binding " + std::to_string(i) + " missing");
+  return b[i].str();
+}
+static const std::string &kern(const Json &op) { return op.at("kernel").str(); }
+
+// Lowering: returns the steps; collects every unsupported op into `errors`.
+static std::vector<Step> lower(const Parsed &pp, bool f16, int L, std::vector<std::string> &errors) {
+  (void)f16;
+  std::vector<Step> steps;
+  const auto &ops = pp.ops;
+  auto k = [&](size_t i) -> std::string { return i < ops.size() ? kern(ops[i]) : std::string(); };
+  for (size_t i = 0; i < ops.size(); i++) {
+    const Json &op = ops[i];
+    const std::string &kn = kern(op);
+    const std::string name = op.at("name").str();
+    const auto &disp = op.at("dispatch").arr();
+    try {
+      Step s;
+      s.name = name;
+      s.kernel = kn;
+      if (kn == "attscore" && k(i + 1) == "attsoftmax" && k(i + 2) == "attpv" &&
+          bind(ops[i + 1], 1) == bind(op, 2) && bind(ops[i + 2], 0) == bind(op, 2)) {
+        // standard attention, split form (src/plan/layers.ts:84-93)
+        s.kind = S_ATTN;
+        s.kernel = "attention";
+        s.in[0].id = bind(op, 0);          // qkv
+        s.in[1].id = bind(ops[i + 2], 4);  // ctx
+        s.H = cint(op, "H");
+        s.D = cint(op, "D");
+        s.scale = (float)cnum(op, "SCALE");
+        s.window = cint(ops[i + 1], "WINDOW");
+        i += 2;
+      } else if (kn == "mbflash" || kn == "mbattention") {
+        s.kind = S_ATTN;
+        s.kernel = "attention";
+        s.in[0].id = bind(op, 0);
+        s.in[1].id = bind(op, 2);
+        s.H = cint(op, "H");
+        s.D = cint(op, "D");
+        s.scale = (float)cnum(op, "SCALE");
+        s.window = cint(op, "WINDOW");
+      } else if (kn == "attrel" && cint(op, "PART") == 0 && k(i + 1) == "attrel" && cint(ops[i + 1], "PART") == 1 &&
+                 k(i + 2) == "attscore" && k(i + 3) == "attsoftrel" && k(i + 4) == "attpv") {
+        // DeBERTa relative attention, split form (src/plan/layers.ts:61-80):
+        // score = (q.k) SCALE + (c2p + p2c) INVSCALE with SCALE = INVSCALE = 1 / sqrt(3 D)
+        s.kind = S_ATTN;
+        s.kernel = "attention-rel";
+        s.rel = true;
+        s.in[0].id = bind(op, 0);           // qkv
+        s.in[1].id = bind(ops[i + 4], 4);   // ctx
+        s.in[2].id = bind(op, 1);           // posKey
+        s.in[3].id = bind(ops[i + 1], 1);   // posQuery
+        s.in[4].id = bind(op, 3);           // relidx
+        s.H = cint(op, "H");
+        s.D = cint(op, "D");
+        s.scale = (float)cnum(ops[i + 3], "INVSCALE");
+        i += 4;
+      } else if (kn == "attention") {
+        // fused DeBERTa attention: score = (q.k + c2p + p2c) / SCALE (src/kernels/attention.wgsl)
+        s.kind = S_ATTN;
+        s.rel = true;
+        s.kernel = "attention-rel";
+        s.in[0].id = bind(op, 0);
+        s.in[1].id = bind(op, 5);
+        s.in[2].id = bind(op, 1);
+        s.in[3].id = bind(op, 2);
+        s.in[4].id = bind(op, 3);
+        s.H = cint(op, "H");
+        s.D = cint(op, "D");
+        s.scale = (float)(1.0 / cnum(op, "SCALE"));
+      } else if (kMatmul.count(kn)) {
+        s.kind = S_GEMM;
+        for (int b = 0; b < 4; b++) s.in[b].id = bind(op, b);
+        s.N = cint(op, "N");
+        s.K = cint(op, "K");
+        s.act = cint(op, "ACT");
+        if (!is_rows_dim(disp.at(1))) {
+          s.seq_rows = true;
+          s.rows_fixed = cint(op, "M");
+        }
+        if (s.act < 0 || s.act > 4) fail(KH_EUNSUPPORTED, "activation " + std::to_string(s.act));
+      } else if (kn == "layernorm") {
+        s.kind = S_LN;
+        for (int b = 0; b < 6; b++) s.in[b].id = bind(op, b);
+        s.N = cint(op, "N");
+        s.mode = cint(op, "MODE");
+        s.eps = (float)cnum(op, "EPS");
+        if (!is_rows_dim(disp.at(0))) {
+          s.seq_rows = true;
+          s.rows_fixed = disp.at(0).integer();
+        }
+        if (s.mode < 0 || s.mode > 2) fail(KH_EUNSUPPORTED, "layernorm MODE " + std::to_string(s.mode));
+      } else if (kn == "embln") {
+        s.kind = S_EMBLN;
+        // word, pos, typ, typeIds, w, bias, mask, out
+        static const int map[6] = {0, 1, 2, 4, 5, 7};
+        for (int b = 0; b < 6; b++) s.in[b].id = bind(op, map[b]);
+        s.markers_id = bind(op, 3);
+        s.N = cint(op, "N");
+        s.offset = cint(op, "OFFSET");
+        s.maxpos = cint(op, "MAXPOS");
+        s.posids = cint(op, "POSIDS");
+        s.eps = (float)cnum(op, "EPS");
+        if (cint(op, "L") != L) fail(KH_EINVAL, "embln L differs from the plan length");
+      } else if (kn == "add") {
+        s.kind = S_ADD;
+        s.in[0].id = bind(op, 0);
+        s.in[1].id = bind(op, 1);
+        s.N = cint(op, "N");
+        s.mode = cint(op, "MODE");
+        if (s.mode != 0 && s.mode != 1) fail(KH_EUNSUPPORTED, "add MODE " + std::to_string(s.mode));
+      } else if (kn == "geglu") {
+        s.kind = S_GEGLU;
+        s.in[0].id = bind(op, 0);
+        s.in[1].id = bind(op, 1);
+        s.I = cint(op, "I");
+      } else if (kn == "rope") {
+        s.kind = S_ROPE;
+        s.in[0].id = bind(op, 0);
+        s.in[1].id = bind(op, 1);
+        s.H = cint(op, "H");
+        s.D = cint(op, "D");
+        if (s.D % 2) fail(KH_EUNSUPPORTED, "rope with odd head dimension");
+      } else if (kn == "pool") {
+        s.kind = S_POOL;
+        s.in[0].id = bind(op, 0);
+        s.in[1].id = bind(op, 2);
+        s.N = cint(op, "N");
+        s.mode = cint(op, "MODE");
+        s.seq_rows = true;
+      } else if (kn == "gather") {
+        s.kind = S_GATHER;
+        s.markers_id = bind(op, 0);
+        s.in[0].id = bind(op, 1);
+        s.in[1].id = bind(op, 2);
+        s.Kmk = cint(op, "K");
+        s.D = cint(op, "D");
+        s.seq_rows = true;
+      } else {
+        fail(KH_EUNSUPPORTED, "kernel " + kn + " has no HIP computation (outside the encoder heads)");
+      }
+      if (s.kind == S_ATTN) {
+        if (s.D != 32 && s.D != 64)
+          fail(KH_EUNSUPPORTED, "attention head dimension " + std::to_string(s.D) + " (32 or 64 supported)");
+      }
+      steps.push_back(std::move(s));
+    } catch (const Error &e) {
+      errors.push_back("op " + name + " (" + kn + "): " + e.what());
+    } catch (const std::runtime_error &e) {
+      errors.push_back("op " + name + " (" + kn + "): " + e.what());
+    }
+  }
+  return steps;
+}
+
+static const Weight *weight_of(kh_ctx *ctx, const std::string &id) {
+  if (id.rfind("w:", 0) != 0) return nullptr;
+  auto it = ctx->weights.find(id.substr(2));
+  return it == ctx->weights.end() ? nullptr : &it->second;
+}
+
+// Checks the weights and buffers every step binds; fills `errors`.
+static void check_bindings(kh_ctx *ctx, const Parsed &pp, const std::vector<Step> &steps, bool f16,
+                           std::vector<std::string> &errors) {
+  std::map<std::string, int64_t> decl;
+  for (const Json &b : pp.root.at("buffers").arr()) decl[b.at("id").str()] = b.at("bytes").integer();
+  const int want = f16 ? KH_F16 : KH_F32;
+  auto need_w = [&](const Step &s, const std::string &id, int64_t count, const char *what) {
+    if (id == "zero" || id == "dummy") return;
+    if (id.rfind("w:", 0) == 0) {
+      const Weight *w = weight_of(ctx, id);
+      if (!w) {
+        errors.push_back("op " + s.name + ": weight " + id.substr(2) + " missing");
+        return;
+      }
+      if (w->dtype != want)
+        errors.push_back("op " + s.name + ": weight " + id.substr(2) + " is not in the plan's storage dtype");
+      if (w->count < count)
+        errors.push_back("op " + s.name + ": weight " + id.substr(2) + " has " + std::to_string(w->count) +
+                         " elements, " + what + " needs " + std::to_string(count));
+      return;
+    }
+    if (!decl.count(id)) errors.push_back("op " + s.name + ": unknown buffer " + id);
+  };
+  for (const Step &s : steps) {
+    switch (s.kind) {
+      case S_GEMM:
+        need_w(s, s.in[1].id, (int64_t)s.N * s.K, "the matmul");
+        need_w(s, s.in[2].id, s.N, "the bias");
+        break;
+      case S_LN:
+        need_w(s, s.in[2].id, s.N, "the norm");
+        need_w(s, s.in[3].id, s.N, "the norm bias");
+        if (s.N > 4096) errors.push_back("op " + s.name + ": LayerNorm width above 4096");
+        break;
+      case S_EMBLN:
+        need_w(s, s.in[1].id, (int64_t)s.maxpos * s.N, "the position table");
+        need_w(s, s.in[3].id, s.N, "the norm");
+        need_w(s, s.in[4].id, s.N, "the norm bias");
+        if (s.N > 4096) errors.push_back("op " + s.name + ": embedding width above 4096");
+        break;
+      case S_ATTN:
+        if (s.rel) {
+          need_w(s, s.in[2].id, 0, "c2p");
+          need_w(s, s.in[3].id, 0, "p2c");
+        }
+        break;
+      default:
+        break;
+    }
+    for (const Ref &r : s.in)
+      if (!r.id.empty() && r.id.rfind("w:", 0) != 0 && r.id != "zero" && r.id != "dummy" && !decl.count(r.id))
+        errors.push_back("op " + s.name + ": unknown buffer " + r.id);
+  }
+}
+
+// ---- execution ---------------------------------------------------------------------------------
+
+using LaunchHook = std::function<void(const Step &, const char *kernel, double flops, double bytes, bool begin)>;
+
+static void *bufp(kh_plan *pl, const Ref &r) { return r.p; }
+
+static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
+  hipStream_t st = pl->stream;
+  const bool f16 = pl->f16;
+  const size_t es = f16 ? 2 : 4;
+  const Packing pk = packing_of(pl);
+  const int64_t rows = s.seq_rows ? (s.kind == S_POOL || s.kind == S_GATHER ? pl->B : s.rows_fixed) : pl->T;
+  auto begin = [&](const char *k, double fl, double by) {
+    if (hook) hook(s, k, fl, by, true);
+  };
+  auto end = [&]() {
+    if (hook) hook(s, nullptr, 0, 0, false);
+  };
+  switch (s.kind) {
+    case S_GEMM: {
+      GemmArgs g;
+      g.a = bufp(pl, s.in[0]);
+      g.lda = s.K;
+      g.w = bufp(pl, s.in[1]);
+      g.ldw = s.K;
+      g.bias = bufp(pl, s.in[2]);
+      g.c = bufp(pl, s.in[3]);
+      g.ldc = s.N;
+      g.M = (int)rows;
+      g.N = s.N;
+      g.K = s.K;
+      g.act = s.act;
+      g.rowdot = s.seq_rows;
+      begin(gemm_uses_mfma(f16, g) ? "gemm_mfma" : "gemm_rowdot", 2.0 * rows * s.N * s.K,
+            (double)es * ((double)rows * s.K + (double)s.N * s.K + (double)rows * s.N + (g.bias ? s.N : 0)));
+      gemm(f16, g, st);
+      end();
+      break;
+    }
+    case S_LN: {
+      const void *b = s.mode == 2 ? bufp(pl, s.in[1]) : nullptr;
+      begin("layernorm", 8.0 * rows * s.N, (double)es * ((s.mode == 2 ? 3.0 : 2.0) * rows * s.N + 2.0 * s.N));
+      layernorm(f16, bufp(pl, s.in[0]), b, bufp(pl, s.in[2]), bufp(pl, s.in[3]), bufp(pl, s.in[5]), rows, s.N, s.eps,
+                st);
+      end();
+      break;
+    }
+    case S_EMBLN: {
+      EmbLnArgs a;
+      a.word = pl->by_ids ? nullptr : bufp(pl, s.in[0]);
+      a.table = pl->by_ids ? pl->ctx->words->p : nullptr;
+      a.ids = pl->by_ids ? (const int32_t *)pl->d_ids.p : nullptr;
+      a.pos = bufp(pl, s.in[1]);
+      a.typ = bufp(pl, s.in[2]);
+      a.tt = pl->in_tt.empty() ? nullptr : (const uint32_t *)pl->d_tt.p;
+      a.gamma = bufp(pl, s.in[3]);
+      a.beta = bufp(pl, s.in[4]);
+      a.out = bufp(pl, s.in[5]);
+      a.N = s.N;
+      a.offset = s.offset;
+      a.maxpos = s.maxpos;
+      a.posids = s.posids;
+      a.eps = s.eps;
+      const int tables = 1 + (a.pos ? 1 : 0) + (a.typ ? 1 : 0);
+      begin("embln", 9.0 * pl->T * s.N, (double)es * (tables + 1.0) * pl->T * s.N + 4.0 * pl->T);
+      embln(f16, a, pk, st);
+      end();
+      break;
+    }
+    case S_ADD:
+      begin("add", (double)pl->T * s.N, 3.0 * es * pl->T * s.N);
+      add(f16, bufp(pl, s.in[0]), bufp(pl, s.in[1]), pl->T, s.N, s.mode, pk, st);
+      end();
+      break;
+    case S_GEGLU:
+      begin("geglu", 20.0 * pl->T * s.I, 3.0 * es * pl->T * s.I);
+      geglu(f16, bufp(pl, s.in[0]), bufp(pl, s.in[1]), pl->T, s.I, st);
+      end();
+      break;
+    case S_ROPE: {
+      const float *table = (const float *)bufp(pl, s.in[1]);
+      begin("rope", 6.0 * pl->T * 2 * s.H * (s.D / 2), 4.0 * es * pl->T * s.H * s.D);
+      rope(f16, bufp(pl, s.in[0]), table, pl->T, s.H, s.D, pl->L, pk, st);
+      end();
+      break;
+    }
+    case S_POOL:
+      begin("pool", (double)pl->T * s.N, (double)es * ((double)pl->T * s.N + (double)pl->B * s.N));
+      pool(f16, bufp(pl, s.in[0]), bufp(pl, s.in[1]), s.N, s.mode, pk, st);
+      end();
+      break;
+    case S_GATHER: {
+      auto it = pl->bufs.find(s.markers_id);
+      const uint32_t *mk = it != pl->bufs.end() && it->second.mem ? (const uint32_t *)it->second.mem->p : nullptr;
+      begin("gather", 0, 2.0 * es * pl->B * s.Kmk * s.D);
+      gather_rows(f16, bufp(pl, s.in[0]), mk, bufp(pl, s.in[1]), s.Kmk, s.D, pk, st);
+      end();
+      break;
+    }
+    case S_ATTN: {
+      AttnArgs a;
+      a.qkv = bufp(pl, s.in[0]);
+      a.ctx = bufp(pl, s.in[1]);
+      a.H = s.H;
+      a.D = s.D;
+      a.scale = s.scale;
+      a.window = s.window;
+      a.tiles = (const int2 *)pl->d_tiles.p;
+      a.ntiles = pl->ntiles;
+      const double hd = (double)s.H * s.D;
+      double pairs = pl->attn_pairs_global;
+      if (s.window > 0) pairs = pl->attn_pairs_window[s.window];
+      if (s.rel) {
+        // c2p = q . posKey[m], p2c = k . posQuery[m] over every bucket row m (relative-position GEMMs)
+        const int nb = pl->rel_nb;
+        GemmArgs g;
+        g.lda = 3 * s.H * s.D;
+        g.ldw = s.H * s.D;
+        g.ldc = (int64_t)s.H * nb;
+        g.M = (int)pl->T;
+        g.N = nb;
+        g.K = s.D;
+        g.act = 0;
+        g.batch = s.H;
+        g.a_bs = s.D;
+        g.w_bs = s.D;
+        g.c_bs = nb;
+        g.c_f32 = true;
+        g.a = a.qkv;
+        g.w = bufp(pl, s.in[2]);
+        g.c = pl->d_c2p.p;
+        const double fl = 2.0 * pl->T * nb * s.D * s.H;
+        const double by = (double)es * (pl->T * hd + (double)nb * hd) + 4.0 * pl->T * s.H * nb;
+        begin("gemm_rel_c2p", fl, by);
+        gemm(f16, g, st);
+        end();
+        g.a = (const char *)a.qkv + (size_t)s.H * s.D * es;
+        g.w = bufp(pl, s.in[3]);
+        g.c = pl->d_p2c.p;
+        begin("gemm_rel_p2c", fl, by);
+        gemm(f16, g, st);
+        end();
+        a.c2p = (const float *)pl->d_c2p.p;
+        a.p2c = (const float *)pl->d_p2c.p;
+        a.bucket = (const int32_t *)pl->d_bucket.p;
+        a.nb = nb;
+        a.lmax = pl->L;
+      }
+      begin(s.rel ? "attention_rel" : "attention", 4.0 * hd * pairs, (double)es * 4.0 * pl->T * hd);
+      attention(f16, a, pk, st);
+      end();
+      break;
+    }
+  }
+}
+
+// ---- packing ----------------------------------------------------------------------------------
+
+static void pack(kh_plan *pl, int rows) {
+  const int L = pl->L, B = pl->B;
+  std::vector<int32_t> n(B);
+  for (int b = 0; b < B; b++) {
+    const float *m = pl->mask_host.data() + (size_t)b * L;
+    int len = 0;
+    while (len < L && m[len] > 0.5f) len++;
+    for (int i = 0; i < L; i++) {
+      const float v = m[i];
+      if (i < len && v != 1.0f)
+        fail(KH_EINVAL, "mask value " + std::to_string(v) + " at sequence " + std::to_string(b) + " row " +
+                            std::to_string(i) + ": the HIP runner takes 0/1 prefix masks");
+      if (i >= len && v > 0.5f)
+        fail(KH_EINVAL, "mask of sequence " + std::to_string(b) + " has a hole before row " + std::to_string(i) +
+                            ": the HIP runner takes prefix masks");
+    }
+    int cap = rows - b * L;
+    cap = cap < 0 ? 0 : (cap > L ? L : cap);
+    n[b] = len < cap ? len : cap;
+  }
+  pl->cu.assign(B + 1, 0);
+  for (int b = 0; b < B; b++) pl->cu[b + 1] = pl->cu[b] + n[b];
+  const int64_t T = pl->cu[B];
+  pl->T = T;
+  std::vector<int32_t> row_pos(T > 0 ? T : 1), row_seq(T > 0 ? T : 1);
+  std::vector<int2> tiles;
+  pl->attn_pairs_global = 0;
+  std::set<int> windows;
+  for (const Step &s : pl->steps)
+    if (s.kind == S_ATTN && s.window > 0) windows.insert(s.window);
+  pl->attn_pairs_window.clear();
+  for (int b = 0; b < B; b++) {
+    for (int i = 0; i < n[b]; i++) {
+      row_pos[pl->cu[b] + i] = i;
+      row_seq[pl->cu[b] + i] = b;
+    }
+    for (int q = 0; q < n[b]; q += ATTN_QTILE) tiles.push_back(make_int2(b, q));
+    pl->attn_pairs_global += (double)n[b] * n[b];
+    for (int w : windows) {
+      double s = 0;
+      for (int i = 0; i < n[b]; i++) {
+        const int lo = std::max(0, i - w), hi = std::min(n[b] - 1, i + w);
+        s += hi - lo + 1;
+      }
+      pl->attn_pairs_window[w] += s;
+    }
+  }
+  pl->ntiles = (int)tiles.size();
+  if (tiles.empty()) tiles.push_back(make_int2(0, 0));
+
+  // metadata: cu | row_pos | row_seq | tiles | tt | ids, one pinned staging block
+  const size_t es = pl->f16 ? 2 : 4;
+  if (pl->d_cu.bytes < (size_t)(B + 1) * 4 || !pl->d_cu.p) pl->d_cu.alloc((size_t)(B + 1) * 4);
+  if (pl->d_row_pos.bytes < (size_t)T * 4 || !pl->d_row_pos.p) pl->d_row_pos.alloc(std::max<int64_t>(T, 1) * 4);
+  if (pl->d_row_seq.bytes < (size_t)T * 4 || !pl->d_row_seq.p) pl->d_row_seq.alloc(std::max<int64_t>(T, 1) * 4);
+  if (pl->d_tiles.bytes < tiles.size() * sizeof(int2) || !pl->d_tiles.p) pl->d_tiles.alloc(tiles.size() * sizeof(int2));
+  KH_CHECK(hipStreamSynchronize(pl->stream));  // staging may still feed an earlier copy
+  const size_t meta = (size_t)(B + 1) * 4 + 2 * (size_t)std::max<int64_t>(T, 1) * 4 + tiles.size() * sizeof(int2) +
+                      (size_t)std::max<int64_t>(T, 1) * 4 * 2;
+  pl->pin_meta.ensure(meta);
+  char *mp = (char *)pl->pin_meta.p;
+  auto put = [&](DevMem &dst, const void *src, size_t bytes) {
+    memcpy(mp, src, bytes);
+    KH_CHECK(hipMemcpyAsync(dst.p, mp, bytes, hipMemcpyHostToDevice, pl->stream));
+    mp += (bytes + 15) & ~(size_t)15;
+  };
+  put(pl->d_cu, pl->cu.data(), (size_t)(B + 1) * 4);
+  put(pl->d_row_pos, row_pos.data(), (size_t)std::max<int64_t>(T, 1) * 4);
+  put(pl->d_row_seq, row_seq.data(), (size_t)std::max<int64_t>(T, 1) * 4);
+  put(pl->d_tiles, tiles.data(), tiles.size() * sizeof(int2));
+  // packed type ids
+  if (!pl->in_tt.empty()) {
+    // type rows the embedding reads must exist (an out-of-range id would read past the table)
+    int64_t type_rows = INT64_MAX;
+    for (const Step &s : pl->steps)
+      if (s.kind == S_EMBLN) {
+        const Weight *w = weight_of(pl->ctx, s.in[2].id);
+        type_rows = w ? w->count / std::max(1, s.N) : (s.in[2].id == "zero" ? 1 : 0);
+      }
+    std::vector<uint32_t> tt(std::max<int64_t>(T, 1), 0u);
+    for (int b = 0; b < B; b++)
+      for (int i = 0; i < n[b]; i++) {
+        const uint32_t v = pl->tt_host.empty() ? 0u : pl->tt_host[(size_t)b * L + i];
+        if ((int64_t)(v & 0xffffu) >= type_rows)
+          fail(KH_EINVAL, "token type " + std::to_string(v & 0xffffu) + " outside the type table");
+        tt[pl->cu[b] + i] = v;
+      }
+    if (pl->d_tt.bytes < tt.size() * 4 || !pl->d_tt.p) pl->d_tt.alloc(tt.size() * 4);
+    put(pl->d_tt, tt.data(), tt.size() * 4);
+  }
+  // packed word rows or ids
+  if (pl->by_ids) {
+    std::vector<int32_t> ids(std::max<int64_t>(T, 1), 0);
+    for (int b = 0; b < B; b++)
+      for (int i = 0; i < n[b]; i++) {
+        const int32_t id = pl->ids_host[(size_t)b * L + i];
+        if (id < 0 || id >= pl->ctx->words_rows)
+          fail(KH_EINVAL, "token id " + std::to_string(id) + " outside the word table");
+        ids[pl->cu[b] + i] = id;
+      }
+    if (pl->d_ids.bytes < ids.size() * 4 || !pl->d_ids.p) pl->d_ids.alloc(ids.size() * 4);
+    put(pl->d_ids, ids.data(), ids.size() * 4);
+  } else {
+    const size_t row = (size_t)pl->E * es;
+    Buffer &eb = pl->bufs.at(pl->in_emb);
+    pl->pin_emb.ensure(std::max<size_t>((size_t)T * row, 16));
+    char *dst = (char *)pl->pin_emb.p;
+    for (int b = 0; b < B; b++) {
+      const size_t src = (size_t)b * L * row;
+      const size_t nb = (size_t)n[b] * row;
+      if (src + nb > pl->emb_host.size()) fail(KH_EINVAL, "word rows shorter than the mask's valid rows");
+      memcpy(dst + (size_t)pl->cu[b] * row, pl->emb_host.data() + src, nb);
+    }
+    if ((size_t)T * row > eb.mem->bytes) fail(KH_EINVAL, "packed rows exceed the emb buffer");
+    if (T > 0) KH_CHECK(hipMemcpyAsync(eb.mem->p, pl->pin_emb.p, (size_t)T * row, hipMemcpyHostToDevice, pl->stream));
+  }
+  pl->dirty = false;
+  pl->last_rows = rows;
+}
+
+static void ensure_rel(kh_plan *pl) {
+  bool rel = false;
+  for (const Step &s : pl->steps) rel = rel || s.rel;
+  if (!rel) return;
+  if (!pl->d_bucket.p) fail(KH_EINVAL, "relative attention needs the relidx table (kh_plan_init_buffer)");
+  int H = 0;
+  for (const Step &s : pl->steps)
+    if (s.rel) H = std::max(H, s.H);
+  const size_t need = (size_t)std::max<int64_t>(pl->T, 1) * H * pl->rel_nb * 4;
+  if (pl->d_c2p.bytes < need) {
+    pl->d_c2p.alloc(need);
+    pl->d_p2c.alloc(need);
+  }
+}
+
+static void run_steps(kh_plan *pl, const LaunchHook &hook) {
+  for (const Step &s : pl->steps) exec_step(pl, s, hook);
+  KH_CHECK(hipGetLastError());
+}
+
+static void latch(kh_ctx *ctx, const Error &e) {
+  if (e.code == KH_EHIP) {
+    hipError_t q = hipGetLastError();
+    (void)q;
+    ctx->lost = true;
+    ctx->lost_msg = e.what();
+  }
+}
+
+}  // namespace kh
+
+// ---- C ABI ------------------------------------------------------------------------------------
+
+#define KH_API_BEGIN try {
+#define KH_API_END                                                      \
+  g_last_error.clear();                                                 \
+  return KH_OK;                                                         \
+  }                                                                     \
+  catch (const kh::Error &e) {                                          \
+    g_last_error = e.what();                                            \
+    return e.code;                                                      \
+  }                                                                     \
+  catch (const std::bad_alloc &) {                                      \
+    g_last_error = "host allocation failed";                            \
+    return KH_ENOMEM;                                                   \
+  }                                                                     \
+  catch (const std::exception &e) {                                     \
+    g_last_error = e.what();                                            \
+    return KH_EINVAL;                                                   \
+  }
+
+static void require_live(kh_ctx *ctx) {
+  if (!ctx) fail(KH_EINVAL, "null context");
+  if (ctx->lost) fail(KH_ELOST, "context lost after an earlier device failure: " + ctx->lost_msg);
+  KH_CHECK(hipSetDevice(ctx->device));
+}
+
+extern "C" {
+
+const char *kh_last_error(void) { return g_last_error.c_str(); }
+int kh_abi_version(void) { return KH_ABI_VERSION; }
+
+int kh_ctx_create(int device, kh_ctx **out) {
+  KH_API_BEGIN
+  if (!out) fail(KH_EINVAL, "null output pointer");
+  int n = 0;
+  KH_CHECK(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) fail(KH_EINVAL, "device " + std::to_string(device) + " of " + std::to_string(n));
+  KH_CHECK(hipSetDevice(device));
+  auto *c = new kh_ctx();
+  c->device = device;
+  *out = c;
+  KH_API_END
+}
+
+int kh_ctx_destroy(kh_ctx *ctx) {
+  KH_API_BEGIN
+  if (ctx) {
+    (void)hipSetDevice(ctx->device);
+    delete ctx;
+  }
+  KH_API_END
+}
+
+int kh_weight_add(kh_ctx *ctx, const char *name, int dtype, const int64_t *shape, int ndim, const void *data,
+                  size_t bytes) {
+  KH_API_BEGIN
+  require_live(ctx);
+  if (!name || !*name) fail(KH_EINVAL, "weight without a name");
+  if (dtype != KH_F32 && dtype != KH_F16 && dtype != KH_U32) fail(KH_EINVAL, "weight dtype " + std::to_string(dtype));
+  if (ndim < 0 || ndim > 8 || (ndim > 0 && !shape)) fail(KH_EINVAL, "weight shape");
+  if (ctx->weights.count(name)) fail(KH_EINVAL, std::string("weight ") + name + " loaded twice");
+  int64_t count = 1;
+  std::vector<int64_t> sh;
+  for (int i = 0; i < ndim; i++) {
+    if (shape[i] < 0) fail(KH_EINVAL, "negative dimension");
+    count *= shape[i];
+    sh.push_back(shape[i]);
+  }
+  if ((size_t)count * elem_size(dtype) != bytes)
+    fail(KH_EINVAL, std::string("weight ") + name + ": " + std::to_string(bytes) + " bytes for " +
+                        std::to_string(count) + " elements");
+  if (bytes && !data) fail(KH_EINVAL, "null weight data");
+  Weight w;
+  w.dtype = dtype;
+  w.shape = sh;
+  w.count = count;
+  w.mem.reset(new DevMem());
+  w.mem->alloc(bytes);
+  if (bytes) KH_CHECK(hipMemcpy(w.mem->p, data, bytes, hipMemcpyHostToDevice));
+  ctx->weight_bytes += bytes;
+  ctx->weights.emplace(name, std::move(w));
+  KH_API_END
+}
+
+int kh_ctx_weight_bytes(const kh_ctx *ctx, uint64_t *out) {
+  KH_API_BEGIN
+  if (!ctx || !out) fail(KH_EINVAL, "null argument");
+  *out = ctx->weight_bytes;
+  KH_API_END
+}
+
+int kh_words_set(kh_ctx *ctx, int dtype, int64_t rows, int64_t width, const void *data, size_t bytes) {
+  KH_API_BEGIN
+  require_live(ctx);
+  if (dtype != KH_F32 && dtype != KH_F16) fail(KH_EINVAL, "word table dtype");
+  if (rows <= 0 || width <= 0 || (size_t)(rows * width) * elem_size(dtype) != bytes || !data)
+    fail(KH_EINVAL, "word table size");
+  ctx->words.reset(new DevMem());
+  ctx->words->alloc(bytes);
+  KH_CHECK(hipMemcpy(ctx->words->p, data, bytes, hipMemcpyHostToDevice));
+  ctx->words_dtype = dtype;
+  ctx->words_rows = rows;
+  ctx->words_width = width;
+  KH_API_END
+}
+
+static std::string join_errors(const std::vector<std::string> &errs) {
+  std::string m;
+  for (const auto &e : errs) m += (m.empty() ? "" : "; ") + e;
+  return m;
+}
+
+int kh_plan_check(kh_ctx *ctx, const char *plan_json, size_t len) {
+  KH_API_BEGIN
+  // a null context checks the plan's structure only (no weights, no device)
+  Parsed pp = parse_plan(plan_json, len);
+  const bool f16 = pp.root.at("f16").kind == Json::Bool && pp.root.at("f16").b;
+  const int L = (int)pp.root.at("length").integer();
+  std::vector<std::string> errors;
+  auto steps = lower(pp, f16, L, errors);
+  if (ctx) check_bindings(ctx, pp, steps, f16, errors);
+  if (pp.root.has("rowSelect") && pp.root.at("rowSelect").kind != Json::Null)
+    errors.push_back("rowSelect (Julia type rows) is outside the encoder heads");
+  if (pp.root.at("inputs").has("markers")) errors.push_back("marker inputs (GLiNER, Julia) are outside the encoder heads");
+  if (!errors.empty()) fail(KH_EUNSUPPORTED, join_errors(errors));
+  KH_API_END
+}
+
+int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out) {
+  KH_API_BEGIN
+  require_live(ctx);
+  if (!out) fail(KH_EINVAL, "null output pointer");
+  Parsed pp = parse_plan(plan_json, len);
+  std::unique_ptr<kh_plan> pl(new kh_plan());
+  pl->ctx = ctx;
+  pl->f16 = pp.root.at("f16").kind == Json::Bool && pp.root.at("f16").b;
+  pl->L = (int)pp.root.at("length").integer();
+  pl->B = (int)pp.root.at("batch").integer();
+  pl->markers = (int)pp.root.at("markers").integer();
+  pl->E = (int)pp.root.at("embeddingSize").integer();
+  if (pl->L <= 0 || pl->B <= 0) fail(KH_EINVAL, "plan length and batch must be positive");
+  std::vector<std::string> errors;
+  pl->steps = lower(pp, pl->f16, pl->L, errors);
+  check_bindings(ctx, pp, pl->steps, pl->f16, errors);
+  const Json &inputs = pp.root.at("inputs");
+  if (inputs.has("markers")) errors.push_back("marker inputs (GLiNER, Julia) are outside the encoder heads");
+  if (!errors.empty()) fail(KH_EUNSUPPORTED, join_errors(errors));
+  pl->in_emb = inputs.at("embeddings").str();
+  pl->in_mask = inputs.at("mask").str();
+  if (inputs.has("typeIds")) pl->in_tt = inputs.at("typeIds").str();
+  const Json &o = pp.root.at("output");
+  pl->out_buf = o.at("buffer").str();
+  pl->out_rows = (int)o.at("rows").integer();
+  pl->out_cols = (int)o.at("cols").integer();
+  if (o.at("dtype").str() != "storage") fail(KH_EUNSUPPORTED, "output dtype " + o.at("dtype").str());
+
+  for (const Json &b : pp.root.at("buffers").arr()) {
+    Buffer buf;
+    buf.bytes = b.at("bytes").integer();
+    buf.usage = b.at("usage").str();
+    pl->bufs.emplace(b.at("id").str(), std::move(buf));
+  }
+  // row spaces and uses
+  pl->bufs.at(pl->in_emb).packed_space = true;
+  for (Step &s : pl->steps) {
+    for (Ref &r : s.in) {
+      if (r.id.empty() || r.id.rfind("w:", 0) == 0 || r.id == "zero" || r.id == "dummy") continue;
+      pl->bufs.at(r.id).used = true;
+    }
+    if (!s.markers_id.empty() && pl->bufs.count(s.markers_id)) pl->bufs.at(s.markers_id).used = true;
+    const std::string *dst = nullptr;
+    switch (s.kind) {
+      case S_GEMM: dst = &s.in[3].id; break;
+      case S_LN: dst = &s.in[5].id; break;
+      case S_EMBLN: dst = &s.in[5].id; break;
+      case S_GEGLU: dst = &s.in[1].id; break;
+      case S_ATTN: dst = &s.in[1].id; break;
+      case S_POOL: dst = &s.in[1].id; break;
+      case S_GATHER: dst = &s.in[1].id; break;
+      default: break;
+    }
+    if (dst) {
+      Buffer &b = pl->bufs.at(*dst);
+      if (s.seq_rows) b.seq_space = true;
+      else b.packed_space = true;
+      if (b.seq_space && b.packed_space) fail(KH_EUNSUPPORTED, "buffer " + *dst + " holds both packed and sequence rows");
+    }
+  }
+  pl->bufs.at(pl->out_buf).used = true;
+  pl->bufs.at(pl->in_emb).used = true;
+  pl->out_packed = pl->bufs.at(pl->out_buf).packed_space;
+  // in-place kernels read what their destination held: the residual stream of a pre-norm layer
+  for (Step &s : pl->steps)
+    if ((s.kind == S_ADD || s.kind == S_ROPE) && pl->bufs.count(s.in[0].id)) pl->bufs.at(s.in[0].id).packed_space = true;
+
+  KH_CHECK(hipSetDevice(ctx->device));
+  KH_CHECK(hipStreamCreateWithFlags(&pl->stream, hipStreamNonBlocking));
+  KH_CHECK(hipEventCreate(&pl->ev0));
+  KH_CHECK(hipEventCreate(&pl->ev1));
+  // relative attention: bucket table per (i - j) from the relidx init table (kh_plan_init_buffer)
+  for (auto &kv : pl->bufs) {
+    Buffer &b = kv.second;
+    const std::string &id = kv.first;
+    if (!b.used) continue;
+    if (id == pl->in_mask || id == "kinfo" || id == "scores" || id == "c2p" || id == "p2c" || id == "dummy") continue;
+    b.mem.reset(new DevMem());
+    b.mem->alloc((size_t)b.bytes);
+    KH_CHECK(hipMemset(b.mem->p, 0, (size_t)b.bytes));
+  }
+  // resolve step pointers
+  for (Step &s : pl->steps) {
+    for (Ref &r : s.in) {
+      if (r.id.empty()) continue;
+      if (r.id == "zero" || r.id == "dummy") {
+        r.p = nullptr;
+      } else if (r.id.rfind("w:", 0) == 0) {
+        const Weight *w = weight_of(ctx, r.id);
+        r.p = w ? w->mem->p : nullptr;
+      } else {
+        Buffer &b = pl->bufs.at(r.id);
+        r.p = b.mem ? b.mem->p : nullptr;
+      }
+    }
+    if (s.kind == S_ATTN && s.rel) {
+      const Weight *pk = weight_of(ctx, s.in[2].id);
+      if (!pk || pk->shape.size() != 2 || pk->shape[1] != (int64_t)s.H * s.D)
+        fail(KH_EINVAL, "op " + s.name + ": position table must be [2 * buckets, H * D]");
+      pl->rel_nb = std::max(pl->rel_nb, (int)pk->shape[0]);
+    }
+  }
+  *out = pl.release();
+  KH_API_END
+}
+
+int kh_plan_init_buffer(kh_plan *plan, const char *id, const void *data, size_t bytes) {
+  KH_API_BEGIN
+  if (!plan || !id) fail(KH_EINVAL, "null argument");
+  require_live(plan->ctx);
+  auto it = plan->bufs.find(id);
+  if (it == plan->bufs.end()) fail(KH_EINVAL, std::string("plan buffer ") + id + " missing");
+  Buffer &b = it->second;
+  if ((int64_t)bytes > b.bytes) fail(KH_EINVAL, std::string("init of ") + id + " larger than the buffer");
+  b.init.assign((const uint8_t *)data, (const uint8_t *)data + bytes);
+  const std::string sid = id;
+  if (sid == "relidx") {
+    // relidx[i][j] depends on i - j only: keep bucket(i - j) for i - j in [-(L-1), L-1]
+    const int L = plan->L;
+    if (bytes != (size_t)L * L * 4) fail(KH_EINVAL, "relidx must hold L * L u32");
+    const uint32_t *t = (const uint32_t *)data;
+    plan->bucket_host.assign(2 * L - 1, 0);
+    for (int d = -(L - 1); d <= L - 1; d++) plan->bucket_host[d + L - 1] = (int32_t)(d >= 0 ? t[(size_t)d * L] : t[-d]);
+    for (int i = 0; i < L; i++)
+      for (int j = 0; j < L; j++)
+        if ((int32_t)t[(size_t)i * L + j] != plan->bucket_host[i - j + L - 1])
+          fail(KH_EUNSUPPORTED, "relidx is not a function of i - j");
+    for (int32_t v : plan->bucket_host)
+      if (v < 0 || v >= plan->rel_nb) fail(KH_EINVAL, "relidx entry outside the position table");
+    plan->d_bucket.alloc(plan->bucket_host.size() * 4);
+    KH_CHECK(hipMemcpy(plan->d_bucket.p, plan->bucket_host.data(), plan->bucket_host.size() * 4, hipMemcpyHostToDevice));
+    return KH_OK;
+  }
+  if (b.mem) KH_CHECK(hipMemcpy(b.mem->p, data, bytes, hipMemcpyHostToDevice));
+  KH_API_END
+}
+
+int kh_plan_info_get(const kh_plan *plan, kh_plan_info *out) {
+  KH_API_BEGIN
+  if (!plan || !out) fail(KH_EINVAL, "null argument");
+  memset(out, 0, sizeof(*out));
+  out->length = plan->L;
+  out->batch = plan->B;
+  out->markers = plan->markers;
+  out->f16 = plan->f16;
+  uint64_t bytes = 0;
+  for (const auto &kv : plan->bufs)
+    if (kv.second.mem) bytes += kv.second.mem->bytes;
+  bytes += plan->d_c2p.bytes + plan->d_p2c.bytes;
+  out->bytes = bytes;
+  out->out_rows = plan->out_rows;
+  out->out_cols = plan->out_cols;
+  int launches = 0;
+  for (const Step &s : plan->steps) launches += (s.kind == S_ATTN && s.rel) ? 3 : 1;
+  out->launches = launches;
+  KH_API_END
+}
+
+static void stage_common(kh_plan *plan, const float *mask, size_t mask_count, const uint32_t *tt, size_t tt_count) {
+  const size_t M = (size_t)plan->L * plan->B;
+  if (!mask || mask_count == 0 || mask_count > M) fail(KH_EINVAL, "mask must hold 1 .. L * B values");
+  plan->mask_host.assign(M, 0.f);
+  memcpy(plan->mask_host.data(), mask, mask_count * 4);
+  plan->tt_host.clear();
+  if (!plan->in_tt.empty()) {
+    if (!tt) fail(KH_EINVAL, "plan needs typeIds");
+    if (tt_count > M) fail(KH_EINVAL, "typeIds longer than the plan");
+    plan->tt_host.assign(M, 0u);
+    memcpy(plan->tt_host.data(), tt, tt_count * 4);
+  }
+  plan->uploaded = true;
+  plan->dirty = true;
+}
+
+int kh_upload(kh_plan *plan, const void *emb, size_t emb_bytes, const float *mask, size_t mask_count,
+              const uint32_t *type_ids, size_t type_count) {
+  KH_API_BEGIN
+  if (!plan) fail(KH_EINVAL, "null plan");
+  require_live(plan->ctx);
+  const auto &eb = plan->bufs.at(plan->in_emb);
+  if (!emb && emb_bytes) fail(KH_EINVAL, "null word rows");
+  if ((int64_t)emb_bytes > eb.bytes)
+    fail(KH_EINVAL, "input emb has " + std::to_string(emb_bytes) + " B, the buffer " + std::to_string(eb.bytes));
+  stage_common(plan, mask, mask_count, type_ids, type_count);
+  plan->emb_host.assign((const uint8_t *)emb, (const uint8_t *)emb + emb_bytes);
+  plan->by_ids = false;
+  KH_API_END
+}
+
+int kh_upload_ids(kh_plan *plan, const int32_t *ids, size_t id_count, const float *mask, size_t mask_count,
+                  const uint32_t *type_ids, size_t type_count) {
+  KH_API_BEGIN
+  if (!plan) fail(KH_EINVAL, "null plan");
+  require_live(plan->ctx);
+  kh_ctx *c = plan->ctx;
+  if (!c->words) fail(KH_EINVAL, "no device word table (kh_words_set)");
+  if (c->words_dtype != (plan->f16 ? KH_F16 : KH_F32) || c->words_width != plan->E)
+    fail(KH_EINVAL, "word table dtype or width differs from the plan");
+  const size_t M = (size_t)plan->L * plan->B;
+  if (!ids || id_count > M) fail(KH_EINVAL, "ids must hold up to L * B values");
+  stage_common(plan, mask, mask_count, type_ids, type_count);
+  plan->ids_host.assign(M, 0);
+  memcpy(plan->ids_host.data(), ids, id_count * 4);
+  plan->by_ids = true;
+  KH_API_END
+}
+
+int kh_run(kh_plan *plan, int32_t rows) {
+  KH_API_BEGIN
+  if (!plan) fail(KH_EINVAL, "null plan");
+  require_live(plan->ctx);
+  if (rows < 1 || rows > plan->L * plan->B)
+    fail(KH_EINVAL, std::to_string(rows) + " rows, the plan has " + std::to_string(plan->L * plan->B));
+  if (!plan->uploaded) fail(KH_EINVAL, "run before upload");
+  try {
+    if (plan->dirty || rows != plan->last_rows) pack(plan, rows);
+    ensure_rel(plan);
+    KH_CHECK(hipEventRecord(plan->ev0, plan->stream));
+    run_steps(plan, nullptr);
+    KH_CHECK(hipEventRecord(plan->ev1, plan->stream));
+    plan->ran = true;
+  } catch (const Error &e) {
+    latch(plan->ctx, e);
+    throw;
+  }
+  KH_API_END
+}
+
+int kh_sync(kh_plan *plan) {
+  KH_API_BEGIN
+  if (!plan) fail(KH_EINVAL, "null plan");
+  require_live(plan->ctx);
+  try {
+    KH_CHECK(hipStreamSynchronize(plan->stream));
+  } catch (const Error &e) {
+    latch(plan->ctx, e);
+    throw;
+  }
+  KH_API_END
+}
+
+int kh_last_run_ms(kh_plan *plan, float *ms) {
+  KH_API_BEGIN
+  if (!plan || !ms) fail(KH_EINVAL, "null argument");
+  if (!plan->ran) fail(KH_EINVAL, "no run yet");
+  KH_CHECK(hipEventSynchronize(plan->ev1));
+  KH_CHECK(hipEventElapsedTime(ms, plan->ev0, plan->ev1));
+  KH_API_END
+}
+
+int kh_packed_rows(const kh_plan *plan, int64_t *out) {
+  KH_API_BEGIN
+  if (!plan || !out) fail(KH_EINVAL, "null argument");
+  *out = plan->T;
+  KH_API_END
+}
+
+int kh_read_output(kh_plan *plan, float *out, size_t count) {
+  KH_API_BEGIN
+  if (!plan || !out) fail(KH_EINVAL, "null argument");
+  require_live(plan->ctx);
+  if (!plan->ran) fail(KH_EINVAL, "read before run");
+  const size_t n = (size_t)plan->out_rows * plan->out_cols;
+  if (count < n) fail(KH_EINVAL, "output holds " + std::to_string(n) + " values, the array " + std::to_string(count));
+  try {
+    Buffer &b = plan->bufs.at(plan->out_buf);
+    const size_t es = plan->f16 ? 2 : 4;
+    const int cols = plan->out_cols;
+    if (!plan->out_packed) {
+      std::vector<uint8_t> raw(n * es);
+      KH_CHECK(hipMemcpyAsync(raw.data(), b.mem->p, n * es, hipMemcpyDeviceToHost, plan->stream));
+      KH_CHECK(hipStreamSynchronize(plan->stream));
+      // sequences without a valid row: zero output (the reference computes them from padding)
+      for (size_t i = 0; i < n; i++) out[i] = plan->f16 ? (float)((const _Float16 *)raw.data())[i] : ((const float *)raw.data())[i];
+      if (plan->out_rows == plan->B)
+        for (int bb = 0; bb < plan->B; bb++)
+          if (plan->cu[bb + 1] == plan->cu[bb]) memset(out + (size_t)bb * cols, 0, (size_t)cols * 4);
+    } else {
+      // token rows: packed row cu[b] + i goes to b * L + i; rows past a sequence are zero
+      const int64_t T = plan->T;
+      std::vector<uint8_t> raw((size_t)std::max<int64_t>(T, 1) * cols * es);
+      if (T > 0) KH_CHECK(hipMemcpyAsync(raw.data(), b.mem->p, (size_t)T * cols * es, hipMemcpyDeviceToHost, plan->stream));
+      KH_CHECK(hipStreamSynchronize(plan->stream));
+      memset(out, 0, n * 4);
+      for (int bb = 0; bb < plan->B; bb++)
+        for (int i = 0; i < plan->cu[bb + 1] - plan->cu[bb]; i++) {
+          const size_t src = ((size_t)plan->cu[bb] + i) * cols, dst = ((size_t)bb * plan->L + i) * cols;
+          if (dst + cols > n) break;
+          for (int c = 0; c < cols; c++)
+            out[dst + c] = plan->f16 ? (float)((const _Float16 *)raw.data())[src + c] : ((const float *)raw.data())[src + c];
+        }
+    }
+  } catch (const Error &e) {
+    latch(plan->ctx, e);
+    throw;
+  }
+  KH_API_END
+}
+
+int kh_profile(kh_plan *plan, int32_t rows, kh_launch_stat *out, int32_t cap, int32_t *count) {
+  KH_API_BEGIN
+  if (!plan || !count) fail(KH_EINVAL, "null argument");
+  require_live(plan->ctx);
+  if (!plan->uploaded) fail(KH_EINVAL, "profile before upload");
+  if (rows < 1 || rows > plan->L * plan->B) fail(KH_EINVAL, "rows outside the plan");
+  if (plan->dirty || rows != plan->last_rows) pack(plan, rows);
+  ensure_rel(plan);
+  struct Rec {
+    std::string name, kernel;
+    double flops, bytes;
+    hipEvent_t a, b;
+  };
+  std::vector<Rec> recs;
+  try {
+    LaunchHook hook = [&](const Step &s, const char *k, double fl, double by, bool begin) {
+      if (begin) {
+        Rec r;
+        r.name = s.name;
+        r.kernel = k;
+        r.flops = fl;
+        r.bytes = by;
+        KH_CHECK(hipEventCreate(&r.a));
+        KH_CHECK(hipEventCreate(&r.b));
+        KH_CHECK(hipEventRecord(r.a, plan->stream));
+        recs.push_back(r);
+      } else {
+        KH_CHECK(hipEventRecord(recs.back().b, plan->stream));
+      }
+    };
+    KH_CHECK(hipEventRecord(plan->ev0, plan->stream));
+    run_steps(plan, hook);
+    KH_CHECK(hipEventRecord(plan->ev1, plan->stream));
+    KH_CHECK(hipStreamSynchronize(plan->stream));
+    plan->ran = true;
+  } catch (const Error &e) {
+    for (auto &r : recs) {
+      (void)hipEventDestroy(r.a);
+      (void)hipEventDestroy(r.b);
+    }
+    latch(plan->ctx, e);
+    throw;
+  }
+  *count = (int32_t)recs.size();
+  for (size_t i = 0; i < recs.size(); i++) {
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, recs[i].a, recs[i].b);
+    if ((int32_t)i < cap && out) {
+      kh_launch_stat &o = out[i];
+      memset(&o, 0, sizeof(o));
+      snprintf(o.name, sizeof(o.name), "%s", recs[i].name.c_str());
+      snprintf(o.kernel, sizeof(o.kernel), "%s", recs[i].kernel.c_str());
+      o.ms = ms;
+      o.flops = recs[i].flops;
+      o.bytes = recs[i].bytes;
+    }
+    (void)hipEventDestroy(recs[i].a);
+    (void)hipEventDestroy(recs[i].b);
+  }
+  KH_API_END
+}
+
+int kh_plan_destroy(kh_plan *plan) {
+  KH_API_BEGIN
+  if (plan) {
+    (void)hipSetDevice(plan->ctx->device);
+    if (plan->stream) (void)hipStreamSynchronize(plan->stream);
+    if (plan->ev0) (void)hipEventDestroy(plan->ev0);
+    if (plan->ev1) (void)hipEventDestroy(plan->ev1);
+    hipStream_t s = plan->stream;
+    delete plan;
+    if (s) (void)hipStreamDestroy(s);
+  }
+  KH_API_END
+}
+
+}  // extern "C"
