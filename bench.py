@@ -1,0 +1,180 @@
+"""Throughput of the encoder hot path on one MI355X: sequences/s and tokens/s of a ragged batch.
+
+A step is one forward of the whole batch plan (embedding + LayerNorm, 12 post-LN layers, CLS head)
+over inputs already resident in HBM. The default workload is BASELINE.json's headline config
+(RoBERTa-base shape, f16 storage / f32 accumulate, 256 sequences with lognormal lengths, median
+45, packed without padding); --workload picks another benchmark config.
+
+Besides the JSON line the bench measures, per launch, GPU time with HIP events on the plan's own
+stream (kh_profile) and reports the dominant kernel against its roofline, and it times the CPU
+oracle (f32 restatement of the reference's WASM executor) on a bounded sample of the same batch.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK = {"f16_mfma_tflops": 2500.0, "f32_mfma_tflops": 157.3, "hbm_gbs": 8000.0}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(w, weights, seconds: float = 12.0) -> dict:
+    """The oracle on the host cores, the reference's WASM schedule (one sequence at a time on the
+    bucket plan, real rows only), threads = min(cores, 8) as the reference's 'auto'
+    (src/wasm-plan-host.ts:35-49), over as many sequences of the batch as fit ~`seconds`."""
+    from kleinhirn_amd import inputs
+    from kleinhirn_amd.plan.build import build_plan
+    from oracle.oracle import OracleRuntime
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(cores or 1, 8))
+    plan = build_plan(w.spec, w.head, w.length, 1, False)
+    rt = OracleRuntime(weights, [plan])
+    p = rt.plan(plan, threads=threads)
+    table = weights["embeddings.word.weight"]
+    ids = w.ids()
+    done = toks = 0
+    t0 = time.perf_counter()
+    for seq in ids:
+        ri = inputs.run_input(w.spec, table, [seq], w.length)
+        p.upload(ri["embeddings"], ri["mask"], ri["typeIds"])
+        p.run(len(seq))
+        p.read_output()
+        done += 1
+        toks += len(seq)
+        if time.perf_counter() - t0 > seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(done / dt, 3), "unit": "sequences/s", "cores": threads, "kind": "port",
+            "tokens_per_s": round(toks / dt, 1),
+            "sample": f"first {done} of {len(ids)} sequences ({toks} tokens), one B=1 bucket plan "
+                      f"(L={w.length}) per sequence, f32, {threads} OpenMP threads of {cores} cores"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3a", "c3b", "c4", "c5"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--ids", action="store_true", help="device word gather (token ids) instead of host rows")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs the path on a single MI355X (no sharding, "
+              f"no collectives); --gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+
+    import torch  # device plumbing only: the hot path is libkh_hip.so
+    from kleinhirn_amd import configs, inputs
+    from kleinhirn_amd.backend import HipBackend
+    from kleinhirn_amd.plan.build import build_plan
+
+    assert torch.cuda.is_available(), "bench needs the GPU"
+    w = configs.ALL[args.workload]()
+    f16 = w.f16
+    t0 = time.perf_counter()
+    weights = configs.make_weights(w.spec, w.head)
+    W = configs.storage(weights, f16)
+    log(f"weights {time.perf_counter() - t0:.1f}s")
+    be = HipBackend(W)
+    plan = build_plan(w.spec, w.head, w.length, w.batch, f16)
+    be.check(plan)
+    r = be.runner(plan)
+    ids = w.ids()
+    rows = w.length * w.batch
+    if args.ids:
+        be.set_words(W["embeddings.word.weight"])
+        mask, tt = inputs.mask_and_types(w.spec, ids, w.length)
+        flat = np.zeros(rows, dtype=np.int32)
+        for b, seq in enumerate(ids):
+            flat[b * w.length:b * w.length + len(seq)] = seq
+        r.upload_ids(flat, mask, tt)
+    else:
+        r.upload(inputs.run_input(w.spec, W["embeddings.word.weight"], ids, w.length))
+    # boundary time of the first call: packing + H2D of the valid rows + forward + readback
+    t0 = time.perf_counter()
+    r.run(rows)
+    out = r.read_output()
+    boundary_ms = (time.perf_counter() - t0) * 1e3
+    assert np.isfinite(out).all()
+    T = r.packed_rows()
+    for _ in range(args.warmup):
+        r.run(rows)
+    r.sync()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        r.run(rows)
+    r.sync()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / max(1, args.steps)
+    seq_s = w.batch / dt
+    tok_s = T / dt
+
+    # per-launch profile (HIP events on the plan's stream) and the dominant kernel's roofline
+    prof = r.profile(rows)
+    by_kernel: dict[str, dict] = {}
+    for p in prof:
+        k = by_kernel.setdefault(p["kernel"], {"ms": 0.0, "flops": 0.0, "bytes": 0.0, "launches": 0})
+        k["ms"] += p["ms"]
+        k["flops"] += p["flops"]
+        k["bytes"] += p["bytes"]
+        k["launches"] += 1
+    total_ms = sum(k["ms"] for k in by_kernel.values())
+    for name, k in sorted(by_kernel.items(), key=lambda kv: -kv[1]["ms"]):
+        tf = k["flops"] / (k["ms"] * 1e-3) / 1e12 if k["ms"] else 0
+        gb = k["bytes"] / (k["ms"] * 1e-3) / 1e9 if k["ms"] else 0
+        log(f"  {name:16s} {k['launches']:4d} launches {k['ms']:8.3f} ms ({100 * k['ms'] / total_ms:5.1f} %) "
+            f"{tf:8.1f} TFLOP/s {gb:8.1f} GB/s")
+    dom_name, dom = max(by_kernel.items(), key=lambda kv: kv[1]["ms"])
+    mfma = dom_name.startswith("gemm") or dom_name.startswith("attention")
+    avg_ms = dom["ms"] / dom["launches"]
+    if mfma:
+        achieved = dom["flops"] / dom["launches"] / (avg_ms * 1e-3) / 1e12
+        peak = PEAK["f16_mfma_tflops"] if f16 else PEAK["f32_mfma_tflops"]
+        roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s"}
+    else:
+        achieved = dom["bytes"] / dom["launches"] / (avg_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK["hbm_gbs"], "unit": "GB/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["traffic"] = None
+    roof["kernel"] = dom_name
+    roof["avg_launch_ms"] = round(avg_ms, 4)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(w, weights, args.cpu_seconds)
+
+    line = {
+        "metric": "sequences/sec + tokens/sec, BERT-base f16 ragged batch; % MFMA / HBM peak",
+        "value": round(seq_s, 1), "unit": "sequences/s", "tokens_per_s": round(tok_s, 1),
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16" if f16 else "f32", "data": "synthetic (seeded LCG ids and N(0,0.02) weights)",
+        "config": {"workload": w.name, "global_batch": w.batch, "tokens": T, "bucket_length": w.length,
+                   "layers": w.spec["layers"], "hidden": w.spec["hidden"], "packed": True,
+                   "word_rows": "device gather" if args.ids else "host gather, uploaded once"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "gpu_kernel_ms": round(total_ms, 4), "first_call_boundary_ms": round(boundary_ms, 2),
+    }
+    print(json.dumps(line), flush=True)
+    r.destroy()
+    be.dispose()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -672,11 +672,14 @@ static void pack(kh_plan *pl, int rows) {
   if (pl->d_row_seq.bytes < (size_t)T * 4 || !pl->d_row_seq.p) pl->d_row_seq.alloc(std::max<int64_t>(T, 1) * 4);
   if (pl->d_tiles.bytes < tiles.size() * sizeof(int2) || !pl->d_tiles.p) pl->d_tiles.alloc(tiles.size() * sizeof(int2));
   KH_CHECK(hipStreamSynchronize(pl->stream));  // staging may still feed an earlier copy
-  const size_t meta = (size_t)(B + 1) * 4 + 2 * (size_t)std::max<int64_t>(T, 1) * 4 + tiles.size() * sizeof(int2) +
-                      (size_t)std::max<int64_t>(T, 1) * 4 * 2;
+  // six blocks at most (cu, row_pos, row_seq, tiles, type ids, ids), each 16-byte aligned
+  const size_t T1 = (size_t)std::max<int64_t>(T, 1);
+  const size_t meta = (size_t)(B + 1) * 4 + 4 * T1 * 4 + tiles.size() * sizeof(int2) + 6 * 16;
   pl->pin_meta.ensure(meta);
   char *mp = (char *)pl->pin_meta.p;
+  char *const mend = mp + meta;
   auto put = [&](DevMem &dst, const void *src, size_t bytes) {
+    if (mp + bytes > mend || bytes > dst.bytes) fail(KH_EINVAL, "internal: packing staging overflow");
     memcpy(mp, src, bytes);
     KH_CHECK(hipMemcpyAsync(dst.p, mp, bytes, hipMemcpyHostToDevice, pl->stream));
     mp += (bytes + 15) & ~(size_t)15;
