@@ -32,7 +32,8 @@ __device__ __forceinline__ float wave_max(float v) {
 // GELU by erf through Abramowitz-Stegun 7.1.26 (the reference's constants, src/wasm/plan.ts:99-107)
 __device__ __forceinline__ float gelu_as(float v) {
   float u = v * 0.7071067811865476f;
-  float t = 1.0f / (1.0f + 0.3275911f * fabsf(u));
+  // hardware reciprocal (1 ulp): the formula's own error is 1.5e-7 absolute
+  float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * fabsf(u));
   float p = (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
              0.254829592f) * t;
   float e = 1.0f - p * __expf(-u * u);

@@ -1,17 +1,33 @@
 // C = act(A W^T + bias) on CDNA4 matrix cores.
 //
 // Both operands are K-contiguous (activations [M, K] row-major, weights PyTorch [N, K] never
-// transposed), which is the layout MFMA fragments want: lane l of a 32x32 tile reads 8 (f16) or 1
-// (f32) consecutive k values of row l % 32. A 256-thread block (4 wavefronts, 2 x 2) computes a
-// 128 x 128 tile; each wavefront holds a 64 x 64 sub-tile as 2 x 2 accumulators of
-// v_mfma_f32_32x32x16_f16 (f16 storage) or v_mfma_f32_32x32x2f32 (f32 storage). The K loop stages
-// 128-byte-wide slabs of A and W through LDS (rows padded by 16 bytes, so the 16-byte fragment
-// reads of 8 consecutive rows hit distinct banks) with a register prefetch of the next slab.
-// f32 accumulation; bias and activation are applied to the finished sum, as in the reference
-// (src/wasm/plan.ts:126-154), then rounded once to the storage type.
+// transposed), the layout MFMA fragments want: lane l of a 32 x 32 tile reads 8 (f16) or 1 (f32)
+// consecutive k values of row l % 32 with one LDS load. A block computes a BM x BN tile with
+// WM x WN wavefronts; each wavefront holds a (BM/WM) x (BN/WN) sub-tile as 32 x 32 accumulators of
+// v_mfma_f32_32x32x16_f16 (f16 storage) or v_mfma_f32_32x32x2f32 (f32 storage).
 //
-// A second kernel computes small or unaligned products (head steps with a handful of output
-// classes) with one wavefront per (row, 4 columns).
+// Operands move global -> LDS with gfx950's direct loads (global_load_lds_dwordx4: each lane's
+// 16 bytes land at LDS base + 16 * lane, no VGPR staging) into a ring of STAGES slabs of 128-byte
+// rows (64 halves / 32 floats of k). The loads of slab i + STAGES - 1 are issued while slab i feeds
+// the MFMAs, so STAGES - 1 slabs of every operand are in flight per CU; one barrier per slab.
+// The 16-byte chunks of each row are XOR-swizzled by row (chunk c of row r sits at c ^ (r & 7)):
+// the lanes of one load instruction fetch the chunks in swizzled order, and the fragment reads of
+// 8 consecutive rows hit 8 different bank groups.
+//
+// Larger wavefront tiles cut LDS traffic per MFMA (a 64 x 64 wavefront tile needs the full LDS
+// bandwidth at the MFMA rate, 128 x 64 needs 3/4 of it); smaller block tiles keep more CUs busy on
+// the short M of a ragged batch. The launcher picks per shape.
+//
+// f32 accumulation; bias and activation (a template parameter, so each kernel carries one
+// activation) are applied to the finished sum, as in the reference (src/wasm/plan.ts:126-154), then
+// rounded once to the storage type. Blocks are mapped XCD-aware: consecutive tiles of one row band
+// land on the same XCD (blocks are dealt round-robin over the 8 XCDs), so the A band is read into
+// one L2.
+//
+// Shapes whose K is not a multiple of the slab fall back to a register-staged variant, and narrow
+// products (head steps with a handful of classes) to one wavefront per (row, 4 columns).
+#include <cstdlib>
+
 #include "kernels.h"
 #include "device.h"
 
@@ -19,19 +35,21 @@ namespace kh {
 
 namespace {
 
-constexpr int BM = 128, BN = 128, NT = 256;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void gbl_void;
 
 template <typename T>
 struct Mfma;
 
 template <>
 struct Mfma<half_t> {
-  static constexpr int BK = 64;      // k per LDS slab
+  static constexpr int BK = 64;      // k per LDS slab (128 bytes)
   static constexpr int KSTEP = 16;   // k per MFMA
-  static constexpr int KLANE = 8;    // k values per lane per MFMA
-  static constexpr int LDK = BK + 8; // padded LDS row (halves)
   typedef half8v frag;
-  __device__ static frag load(const half_t *p) { return *reinterpret_cast<const half8v *>(p); }
+  __device__ static frag lds(const char *slab, int row, int kk, int g) {
+    const int chunk = (kk * 2 + g) ^ (row & 7);
+    return *reinterpret_cast<const half8v *>(slab + row * 128 + chunk * 16);
+  }
   __device__ static float16v mma(frag a, frag b, float16v c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
@@ -41,132 +59,311 @@ template <>
 struct Mfma<float> {
   static constexpr int BK = 32;
   static constexpr int KSTEP = 2;
-  static constexpr int KLANE = 1;
-  static constexpr int LDK = BK + 4;
   typedef float frag;
-  __device__ static frag load(const float *p) { return *p; }
+  __device__ static frag lds(const char *slab, int row, int kk, int g) {
+    const int k = kk * 2 + g;
+    const int chunk = (k >> 2) ^ (row & 7);
+    return *reinterpret_cast<const float *>(slab + row * 128 + chunk * 16 + (k & 3) * 4);
+  }
   __device__ static float16v mma(frag a, frag b, float16v c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
   }
 };
 
-// 16-byte chunk of a row
-template <typename T>
-struct Chunk {
-  static constexpr int ELEMS = 16 / sizeof(T);
-  typedef half8v vec_h;
-  typedef float4v vec_f;
-};
+template <int ACT>
+__device__ __forceinline__ float act_fn(float v) {
+  if constexpr (ACT == 1) return fmaxf(v, 0.0f);
+  else if constexpr (ACT == 2) return gelu_as(v);
+  else if constexpr (ACT == 3) return tanhf(v);
+  else if constexpr (ACT == 4) return v / (1.0f + __expf(-v));
+  else return v;
+}
 
-template <typename T>
-__global__ void __launch_bounds__(NT, 2) gemm_mfma_kernel(GemmArgs g, int tiles_n) {
+__device__ __forceinline__ int xcd_tile(int tile, int nblk) {
+  // block b runs on XCD b % 8; give each XCD a contiguous range of tiles
+  const int per = (nblk + 7) / 8;
+  const int x = tile % 8, i = tile / 8;
+  const int full = nblk - (per - 1) * 8;  // XCDs that hold `per` tiles (the rest hold per - 1)
+  return x < full ? x * per + i : full * per + (x - full) * (per - 1) + i;
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int ACT, int FM, int FN>
+__device__ __forceinline__ void epilogue(const GemmArgs &g, float16v (&acc)[FM][FN], int m0, int n0, int wm,
+                                         int wn, int lane, int z) {
+  constexpr int TM = BM / WM, TN = BN / WN;
+  const int lg = lane >> 5;
+  const T *bias = (const T *)g.bias;
+#pragma unroll
+  for (int j = 0; j < FN; j++) {
+    const int col = n0 + wn * TN + j * 32 + (lane & 31);
+    if (col >= g.N) continue;
+    const float bv = bias ? (float)bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = m0 + wm * TM + i * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+        if (row >= g.M) continue;
+        const float v = act_fn<ACT>(acc[i][j][r] + bv);
+        const int64_t o = (int64_t)z * g.c_bs + (int64_t)row * g.ldc + col;
+        if (g.c_f32) ((float *)g.c)[o] = v;
+        else ((T *)g.c)[o] = (T)v;
+      }
+    }
+  }
+}
+
+// f16 epilogue through LDS: each wavefront writes its finished outputs into a row-major BM x BN
+// tile (the operand ring is free after the K loop), then the block stores whole 16-byte chunks of
+// rows, so a wavefront store instruction covers full 128-byte lines instead of 64-byte halves.
+// Needs N % 8 == 0, ldc % 8 == 0 and BM * BN * 2 bytes of LDS.
+template <int BM, int BN, int WM, int WN, int ACT, int FM, int FN>
+__device__ __forceinline__ void epilogue_lds(const GemmArgs &g, float16v (&acc)[FM][FN], int m0, int n0, int wm,
+                                             int wn, int lane, int z, char *smem) {
+  constexpr int TM = BM / WM, TN = BN / WN, NT = 64 * WM * WN;
+  constexpr int RB = BN * 2;  // bytes per LDS row
+  const int lg = lane >> 5;
+  const half_t *bias = (const half_t *)g.bias;
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // the ring is no longer read
+#pragma unroll
+  for (int j = 0; j < FN; j++) {
+    const int c = wn * TN + j * 32 + (lane & 31);
+    const int col = n0 + c;
+    const float bv = bias && col < g.N ? (float)bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = wm * TM + i * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+        // 16-byte chunks of a row rotated by row, so the 2-byte writes of 2 rows spread over banks
+        const int chunk = ((c >> 3) + row) & (BN / 8 - 1);
+        *reinterpret_cast<half_t *>(smem + row * RB + chunk * 16 + (c & 7) * 2) = (half_t)act_fn<ACT>(acc[i][j][r] + bv);
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int CPR = BN / 8;  // chunks per row
+  half_t *C = (half_t *)g.c + (int64_t)z * g.c_bs;
+#pragma unroll
+  for (int q = threadIdx.x; q < BM * CPR; q += NT) {
+    const int row = q / CPR, cc = q % CPR;
+    const int grow = m0 + row, gcol = n0 + cc * 8;
+    if (grow < g.M && gcol < g.N) {
+      const int chunk = (cc + row) & (CPR - 1);
+      *reinterpret_cast<uint4 *>(C + (int64_t)grow * g.ldc + gcol) =
+          *reinterpret_cast<const uint4 *>(smem + row * RB + chunk * 16);
+    }
+  }
+}
+
+// LDS-DMA pipeline kernel; needs K % BK == 0.
+// occupancy the kernel is built for: blocks per CU that fit the LDS ring (160 KB), wavefronts per SIMD;
+// the register allocator may then keep a whole slab's fragments in flight
+template <int BM, int BN, int WM, int WN, int STAGES>
+constexpr int waves_per_simd() {
+  const int blocks = (160 * 1024) / (STAGES * (BM + BN) * 128);
+  const int w = blocks * WM * WN / 4;
+  return w < 1 ? 1 : (w > 2 ? 2 : w);
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int ACT>
+__global__ void __launch_bounds__(64 * WM * WN)
+__attribute__((amdgpu_waves_per_eu(waves_per_simd<BM, BN, WM, WN, STAGES>(), waves_per_simd<BM, BN, WM, WN, STAGES>())))
+gemm_dma_kernel(GemmArgs g, int tiles_m, int tiles_n) {
   typedef Mfma<T> MF;
-  constexpr int BK = MF::BK, LDK = MF::LDK, CE = Chunk<T>::ELEMS;
-  constexpr int CPR = BK / CE;             // 16-byte chunks per slab row (8)
-  constexpr int LOADS = BM * CPR / NT;     // chunks per thread per operand (4)
-  __shared__ __attribute__((aligned(16))) T sA[BM * LDK];
-  __shared__ __attribute__((aligned(16))) T sB[BN * LDK];
+  constexpr int NW = WM * WN;
+  constexpr int BK = MF::BK;
+  constexpr int CE = 16 / sizeof(T);
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int GROUPS = (BM + BN) / 8;        // 8-row groups (1 KB each) per slab
+  constexpr int P = GROUPS / NW;               // load instructions per wavefront per slab
+  static_assert(P * NW == GROUPS, "row groups must split evenly over the wavefronts");
+  static_assert((STAGES - 2) * P <= 63, "vmcnt range");
+  constexpr int STAGE = (BM + BN) * 128;
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
 
   const int z = blockIdx.z;
   const T *A = (const T *)g.a + (int64_t)z * g.a_bs;
   const T *W = (const T *)g.w + (int64_t)z * g.w_bs;
-
-  // tile order: consecutive blocks share the A row block (n fastest)
-  const int tile = blockIdx.x;
+  const int tile = xcd_tile(blockIdx.x, tiles_m * tiles_n);
   const int m0 = (tile / tiles_n) * BM;
   const int n0 = (tile % tiles_n) * BN;
 
-  const int t = threadIdx.x;
-  const int lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int crow = t / CPR, ccol = (t % CPR) * CE;  // chunk row (+32 i) and column
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int lg = lane >> 5;
 
-  typedef uint4 raw;  // 16 bytes
-  raw ra[LOADS], rb[LOADS];
-
-  auto gload = [&](int k0) {
+  // this lane's source rows for its P load instructions (row clamped to the matrix)
+  const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+  const T *src[P];
 #pragma unroll
-    for (int i = 0; i < LOADS; i++) {
-      int r = crow + i * (NT / CPR);
-      int kk = k0 + ccol;
-      int am = m0 + r < g.M ? m0 + r : g.M - 1;
-      int bn = n0 + r < g.N ? n0 + r : g.N - 1;
-      if (kk < g.K) {
-        ra[i] = *reinterpret_cast<const raw *>(A + (int64_t)am * g.lda + kk);
-        rb[i] = *reinterpret_cast<const raw *>(W + (int64_t)bn * g.ldw + kk);
-      } else {
-        ra[i] = make_uint4(0, 0, 0, 0);
-        rb[i] = make_uint4(0, 0, 0, 0);
-      }
+  for (int p = 0; p < P; p++) {
+    const int grp = wave * P + p;
+    const int r = grp * 8 + lrow;  // row inside the A | W slab
+    if (r < BM) {
+      const int m = m0 + r < g.M ? m0 + r : g.M - 1;
+      src[p] = A + (int64_t)m * g.lda + lchunk * CE;
+    } else {
+      const int n = n0 + (r - BM) < g.N ? n0 + (r - BM) : g.N - 1;
+      src[p] = W + (int64_t)n * g.ldw + lchunk * CE;
     }
-  };
-  auto sstore = [&]() {
+  }
+  auto issue = [&](int stage, int k0) {
+    char *base = smem + stage * STAGE;
 #pragma unroll
-    for (int i = 0; i < LOADS; i++) {
-      int r = crow + i * (NT / CPR);
-      *reinterpret_cast<raw *>(&sA[r * LDK + ccol]) = ra[i];
-      *reinterpret_cast<raw *>(&sB[r * LDK + ccol]) = rb[i];
+    for (int p = 0; p < P; p++) {
+      const int grp = wave * P + p;
+      __builtin_amdgcn_global_load_lds((gbl_void *)(src[p] + k0), (lds_void *)(base + grp * 1024), 16, 0, 0);
     }
   };
 
-  float16v acc[2][2];
+  float16v acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < FM; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < FN; j++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-  const int arow = wm * 64 + (lane & 31);
-  const int brow = wn * 64 + (lane & 31);
-  const int kl = (lane >> 5) * MF::KLANE;
+  const int arow = wm * TM + (lane & 31);
+  const int brow = BM + wn * TN + (lane & 31);
+  const int nk = g.K / BK;
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; s++)
+    if (s < nk) issue(s, s * BK);
 
+  for (int it = 0; it < nk; it++) {
+    // Slab `it` complete for this wavefront (later slabs may stay in flight), then a barrier: every
+    // wavefront's part of slab `it` landed and slab it-1 is no longer read. Written as one asm
+    // block: __syncthreads() would add a release fence, i.e. a wait for every outstanding load.
+    if (it + STAGES - 2 < nk) {
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((STAGES - 2) * P) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    if (it + STAGES - 1 < nk) issue((it + STAGES - 1) % STAGES, (it + STAGES - 1) * BK);
+    const char *slab = smem + (it % STAGES) * STAGE;
+    // every fragment read of the slab is issued first; LDS answers in order, so the MFMAs of step
+    // kk wait only for the reads of step kk (partial lgkmcnt waits)
+    constexpr int KK = BK / MF::KSTEP;
+    typename MF::frag af[KK][FM], bf[KK][FN];
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++) {
+#pragma unroll
+      for (int i = 0; i < FM; i++) af[kk][i] = MF::lds(slab, arow + i * 32, kk, lg);
+#pragma unroll
+      for (int j = 0; j < FN; j++) bf[kk][j] = MF::lds(slab, brow + j * 32, kk, lg);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] = MF::mma(af[kk][i], bf[kk][j], acc[i][j]);
+  }
+  if constexpr (sizeof(T) == 2) {
+    if (!g.c_f32 && g.N % 8 == 0 && g.ldc % 8 == 0) {
+      epilogue_lds<BM, BN, WM, WN, ACT>(g, acc, m0, n0, wm, wn, lane, z, smem);
+      return;
+    }
+  }
+  epilogue<T, BM, BN, WM, WN, ACT>(g, acc, m0, n0, wm, wn, lane, z);
+}
+
+// Register-staged variant for any K % 8 (f16) / K % 4 (f32): 128 x 128 tiles, two LDS stages.
+template <typename T, int ACT>
+__global__ void __launch_bounds__(256) gemm_reg_kernel(GemmArgs g, int tiles_m, int tiles_n) {
+  typedef Mfma<T> MF;
+  constexpr int BM = 128, BN = 128, WM = 2, WN = 2, NT = 256;
+  constexpr int BK = MF::BK;
+  constexpr int CE = 16 / sizeof(T);
+  constexpr int TM = 64, TN = 64, FM = 2, FN = 2;
+  constexpr int LA = BM * 8 / NT, LB = BN * 8 / NT;
+  constexpr int STAGE = (BM + BN) * 128;
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+  const int z = blockIdx.z;
+  const T *A = (const T *)g.a + (int64_t)z * g.a_bs;
+  const T *W = (const T *)g.w + (int64_t)z * g.w_bs;
+  const int tile = xcd_tile(blockIdx.x, tiles_m * tiles_n);
+  const int m0 = (tile / tiles_n) * BM;
+  const int n0 = (tile % tiles_n) * BN;
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int lg = lane >> 5;
+
+  uint4 ra[LA], rb[LB];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < LA; i++) {
+      const int q = t + i * NT, r = q >> 3, c = q & 7;
+      const int kk = k0 + c * CE;
+      const int am = m0 + r < g.M ? m0 + r : g.M - 1;
+      const uint4 v = *reinterpret_cast<const uint4 *>(A + (int64_t)am * g.lda + (kk < g.K ? kk : 0));
+      ra[i] = kk < g.K ? v : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < LB; i++) {
+      const int q = t + i * NT, r = q >> 3, c = q & 7;
+      const int kk = k0 + c * CE;
+      const int bn = n0 + r < g.N ? n0 + r : g.N - 1;
+      const uint4 v = *reinterpret_cast<const uint4 *>(W + (int64_t)bn * g.ldw + (kk < g.K ? kk : 0));
+      rb[i] = kk < g.K ? v : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto sstore = [&](int stage) {
+    char *sa = smem + stage * STAGE;
+    char *sb = sa + BM * 128;
+#pragma unroll
+    for (int i = 0; i < LA; i++) {
+      const int q = t + i * NT, r = q >> 3, c = q & 7;
+      *reinterpret_cast<uint4 *>(sa + r * 128 + ((c ^ (r & 7)) << 4)) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < LB; i++) {
+      const int q = t + i * NT, r = q >> 3, c = q & 7;
+      *reinterpret_cast<uint4 *>(sb + r * 128 + ((c ^ (r & 7)) << 4)) = rb[i];
+    }
+  };
+
+  float16v acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+  const int arow = wm * TM + (lane & 31);
+  const int brow = BM + wn * TN + (lane & 31);
   gload(0);
-  sstore();
+  sstore(0);
   __syncthreads();
-  for (int k0 = 0; k0 < g.K; k0 += BK) {
-    const bool more = k0 + BK < g.K;
-    if (more) gload(k0 + BK);
+  int stage = 0;
+  const int nk = (g.K + BK - 1) / BK;
+  for (int it = 0; it < nk; it++) {
+    const bool more = it + 1 < nk;
+    if (more) gload((it + 1) * BK);
+    const char *slab = smem + stage * STAGE;
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += MF::KSTEP) {
-      typename MF::frag af[2], bf[2];
+    for (int kk = 0; kk < BK / MF::KSTEP; kk++) {
+      typename MF::frag af[FM], bf[FN];
 #pragma unroll
-      for (int i = 0; i < 2; i++) af[i] = MF::load(&sA[(arow + i * 32) * LDK + kk + kl]);
+      for (int i = 0; i < FM; i++) af[i] = MF::lds(slab, arow + i * 32, kk, lg);
 #pragma unroll
-      for (int j = 0; j < 2; j++) bf[j] = MF::load(&sB[(brow + j * 32) * LDK + kk + kl]);
+      for (int j = 0; j < FN; j++) bf[j] = MF::lds(slab, brow + j * 32, kk, lg);
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = MF::mma(af[i], bf[j], acc[i][j]);
+        for (int j = 0; j < FN; j++) acc[i][j] = MF::mma(af[i], bf[j], acc[i][j]);
     }
+    if (more) sstore(stage ^ 1);
     __syncthreads();
-    if (more) {
-      sstore();
-      __syncthreads();
-    }
+    stage ^= 1;
   }
-
-  // epilogue: lane l holds column l % 32 and rows 8 (r / 4) + 4 (l / 32) + r % 4 of each 32 x 32
-  const T *bias = (const T *)g.bias;
-#pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int col = n0 + wn * 64 + j * 32 + (lane & 31);
-    if (col >= g.N) continue;
-    const float bv = bias ? (float)bias[col] : 0.f;
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row >= g.M) continue;
-        const float v = activate(acc[i][j][r] + bv, g.act);
-        if (g.c_f32)
-          ((float *)g.c)[(int64_t)z * g.c_bs + (int64_t)row * g.ldc + col] = v;
-        else
-          ((T *)g.c)[(int64_t)z * g.c_bs + (int64_t)row * g.ldc + col] = (T)v;
-      }
-    }
-  }
+  epilogue<T, BM, BN, WM, WN, ACT>(g, acc, m0, n0, wm, wn, lane, z);
 }
 
 // One wavefront per (row m, 4 columns): lanes stride over k, then a wavefront reduction.
@@ -202,26 +399,94 @@ __global__ void __launch_bounds__(256) gemm_rowdot_kernel(GemmArgs g) {
   }
 }
 
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+template <typename K>
+void set_smem(K kernel, int bytes) {
+  (void)hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int ACT>
+void launch_dma(const GemmArgs &g, hipStream_t s) {
+  const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+  constexpr int smem = STAGES * (BM + BN) * 128;
+  static bool configured = false;
+  if (!configured) {
+    set_smem(gemm_dma_kernel<T, BM, BN, WM, WN, STAGES, ACT>, smem);
+    configured = true;
+  }
+  dim3 grid((unsigned)(tm * tn), 1, (unsigned)g.batch);
+  hipLaunchKernelGGL((gemm_dma_kernel<T, BM, BN, WM, WN, STAGES, ACT>), grid, dim3(64 * WM * WN), smem, s, g, tm,
+                     tn);
+}
+
+template <typename T, int ACT>
+void launch_reg(const GemmArgs &g, hipStream_t s) {
+  const int tm = (g.M + 127) / 128, tn = (g.N + 127) / 128;
+  constexpr int smem = 2 * 256 * 128;
+  static bool configured = false;
+  if (!configured) {
+    set_smem(gemm_reg_kernel<T, ACT>, smem);
+    configured = true;
+  }
+  dim3 grid((unsigned)(tm * tn), 1, (unsigned)g.batch);
+  hipLaunchKernelGGL((gemm_reg_kernel<T, ACT>), grid, dim3(256), smem, s, g, tm, tn);
+}
+
+constexpr int CUS = 256;
+
+// DMA tile configurations: 0 = 256x256 (8 wavefronts of 128x64, 2 stages), 1 = 256x128 (4 of
+// 128x64, 3 stages), 2 = 128x128 (4 of 64x64, 4 stages), 3 = 128x128 (4 of 64x64, 2 stages, two
+// blocks per CU), 4 = 256x256 (4 of 128x128, 2 stages). KH_GEMM_TILE forces one (tuning runs).
+int pick_tile(const GemmArgs &g) {
+  const char *e = getenv("KH_GEMM_TILE");
+  const int forced = e ? atoi(e) : -1;
+  if (forced >= 0 && forced <= 4) return forced;
+  auto blocks = [&](int bm, int bn) { return (int64_t)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * g.batch; };
+  if (blocks(256, 256) >= 2 * CUS) return 0;
+  if (blocks(256, 128) >= 2 * CUS) return 1;
+  return 3;
+}
+
+template <typename T, int ACT>
+void launch_act(const GemmArgs &g, hipStream_t s) {
+  if (g.K % Mfma<T>::BK != 0) {
+    launch_reg<T, ACT>(g, s);
+    return;
+  }
+  switch (pick_tile(g)) {
+    case 0: launch_dma<T, 256, 256, 2, 4, 2, ACT>(g, s); break;
+    case 1: launch_dma<T, 256, 128, 2, 2, 3, ACT>(g, s); break;
+    case 2: launch_dma<T, 128, 128, 2, 2, 4, ACT>(g, s); break;
+    case 4: launch_dma<T, 256, 256, 2, 2, 2, ACT>(g, s); break;
+    default: launch_dma<T, 128, 128, 2, 2, 2, ACT>(g, s); break;
+  }
+}
+
 template <typename T>
-bool aligned16(const void *p) {
-  return ((uintptr_t)p & 15) == 0;
+void launch_mfma(const GemmArgs &g, hipStream_t s) {
+  switch (g.act) {
+    case 1: launch_act<T, 1>(g, s); break;
+    case 2: launch_act<T, 2>(g, s); break;
+    case 3: launch_act<T, 3>(g, s); break;
+    case 4: launch_act<T, 4>(g, s); break;
+    default: launch_act<T, 0>(g, s); break;
+  }
 }
 
 }  // namespace
 
 bool gemm_uses_mfma(bool f16, const GemmArgs &g) {
   const int ce = f16 ? 8 : 4;
-  return !g.rowdot && g.N >= 32 && g.K % ce == 0 && g.lda % ce == 0 && g.ldw % ce == 0 &&
-         g.a_bs % ce == 0 && g.w_bs % ce == 0 && aligned16<char>(g.a) && aligned16<char>(g.w);
+  return !g.rowdot && g.N >= 32 && g.K % ce == 0 && g.lda % ce == 0 && g.ldw % ce == 0 && g.a_bs % ce == 0 &&
+         g.w_bs % ce == 0 && aligned16(g.a) && aligned16(g.w);
 }
 
 void gemm(bool f16, const GemmArgs &g, hipStream_t s) {
   if (g.M <= 0 || g.N <= 0 || g.batch <= 0) return;
   if (gemm_uses_mfma(f16, g)) {
-    const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
-    dim3 grid((unsigned)(tm * tn), 1, (unsigned)g.batch);
-    if (f16) hipLaunchKernelGGL((gemm_mfma_kernel<half_t>), grid, dim3(NT), 0, s, g, tn);
-    else hipLaunchKernelGGL((gemm_mfma_kernel<float>), grid, dim3(NT), 0, s, g, tn);
+    if (f16) launch_mfma<half_t>(g, s);
+    else launch_mfma<float>(g, s);
   } else {
     const int64_t waves = (int64_t)g.M * ((g.N + 3) / 4);
     dim3 grid((unsigned)((waves + 3) / 4), 1, (unsigned)g.batch);
