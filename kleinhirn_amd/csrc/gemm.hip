@@ -26,6 +26,7 @@
 //
 // Shapes whose K is not a multiple of the slab fall back to a register-staged variant, and narrow
 // products (head steps with a handful of classes) to one wavefront per (row, 4 columns).
+#include <algorithm>
 #include <cstdlib>
 
 #include "kernels.h"
@@ -272,6 +273,134 @@ gemm_dma_kernel(GemmArgs g, int tiles_m, int tiles_n) {
   epilogue<T, BM, BN, WM, WN, ACT>(g, acc, m0, n0, wm, wn, lane, z);
 }
 
+// Persistent variant: a fixed grid of blocks walks the tiles (block b takes tiles b, b + G, ...),
+// and the slab ring runs continuously over the block's (tile, k) sequence, so the first slabs of
+// the next tile are in flight while the current tile's last MFMAs and its epilogue run. The
+// epilogue stores straight from the accumulators (the ring stays busy). Needs K % BK == 0.
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int ACT>
+__global__ void __launch_bounds__(64 * WM * WN)
+__attribute__((amdgpu_waves_per_eu(waves_per_simd<BM, BN, WM, WN, STAGES>(), waves_per_simd<BM, BN, WM, WN, STAGES>())))
+gemm_persist_kernel(GemmArgs g, int tiles_m, int tiles_n) {
+  typedef Mfma<T> MF;
+  constexpr int NW = WM * WN;
+  constexpr int BK = MF::BK;
+  constexpr int CE = 16 / sizeof(T);
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int KK = BK / MF::KSTEP;
+  constexpr int GROUPS = (BM + BN) / 8;
+  constexpr int P = GROUPS / NW;
+  static_assert(P * NW == GROUPS, "row groups must split evenly over the wavefronts");
+  static_assert((STAGES - 2) * P <= 63, "vmcnt range");
+  constexpr int STAGE = (BM + BN) * 128;
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+  const int ntiles = tiles_m * tiles_n;
+  const int G = gridDim.x;
+  const int b = blockIdx.x;
+  const int my_tiles = b < ntiles ? (ntiles - 1 - b) / G + 1 : 0;
+  const int nk = g.K / BK;
+  const int total = my_tiles * nk;
+  const T *A = (const T *)g.a;
+  const T *W = (const T *)g.w;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int lg = lane >> 5;
+  const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+
+  auto tile_of = [&](int j, int &m0, int &n0) {
+    const int t = xcd_tile(b + j * G, ntiles);
+    m0 = (t / tiles_n) * BM;
+    n0 = (t % tiles_n) * BN;
+  };
+  // global iteration q = (j, k): slab k of the block's j-th tile
+  auto issue = [&](int q) {
+    const int j = q / nk, k0 = (q - j * nk) * BK;
+    int m0, n0;
+    tile_of(j, m0, n0);
+    char *base = smem + (q % STAGES) * STAGE;
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+      const int grp = wave * P + p;
+      const int r = grp * 8 + lrow;
+      const T *src;
+      if (r < BM) {
+        const int m = m0 + r < g.M ? m0 + r : g.M - 1;
+        src = A + (int64_t)m * g.lda + lchunk * CE + k0;
+      } else {
+        const int n = n0 + (r - BM) < g.N ? n0 + (r - BM) : g.N - 1;
+        src = W + (int64_t)n * g.ldw + lchunk * CE + k0;
+      }
+      __builtin_amdgcn_global_load_lds((gbl_void *)src, (lds_void *)(base + grp * 1024), 16, 0, 0);
+    }
+  };
+
+  float16v acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int jj = 0; jj < FN; jj++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][jj][r] = 0.f;
+
+  const int arow = wm * TM + (lane & 31);
+  const int brow = BM + wn * TN + (lane & 31);
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; s++)
+    if (s < total) issue(s);
+
+  for (int q = 0; q < total; q++) {
+    if (q + STAGES - 2 < total) {
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((STAGES - 2) * P) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    if (q + STAGES - 1 < total) issue(q + STAGES - 1);
+    const char *slab = smem + (q % STAGES) * STAGE;
+    typename MF::frag af[2][FM], bf[2][FN];
+    auto rd = [&](int kk, int s) {
+#pragma unroll
+      for (int i = 0; i < FM; i++) af[s][i] = MF::lds(slab, arow + i * 32, kk, lg);
+#pragma unroll
+      for (int jj = 0; jj < FN; jj++) bf[s][jj] = MF::lds(slab, brow + jj * 32, kk, lg);
+    };
+    rd(0, 0);
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++) {
+      if (kk + 1 < KK) rd(kk + 1, (kk + 1) & 1);
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int jj = 0; jj < FN; jj++) acc[i][jj] = MF::mma(af[kk & 1][i], bf[kk & 1][jj], acc[i][jj]);
+    }
+    // schedule: DMA issue, reads of step 0, then the reads of step kk + 1 spread between the MFMAs
+    // of step kk
+    __builtin_amdgcn_sched_group_barrier(0x020, P, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);
+#pragma unroll
+    for (int kk = 0; kk < KK - 1; kk++) {
+#pragma unroll
+      for (int r = 0; r < FM + FN; r++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, (FM * FN + FM + FN - 1) / (FM + FN), 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);
+    if ((q + 1) % nk == 0) {
+      int m0, n0;
+      tile_of(q / nk, m0, n0);
+      epilogue<T, BM, BN, WM, WN, ACT>(g, acc, m0, n0, wm, wn, lane, 0);
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int jj = 0; jj < FN; jj++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) acc[i][jj][r] = 0.f;
+    }
+  }
+}
+
 // Register-staged variant for any K % 8 (f16) / K % 4 (f32): 128 x 128 tiles, two LDS stages.
 template <typename T, int ACT>
 __global__ void __launch_bounds__(256) gemm_reg_kernel(GemmArgs g, int tiles_m, int tiles_n) {
@@ -420,6 +549,20 @@ void launch_dma(const GemmArgs &g, hipStream_t s) {
                      tn);
 }
 
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int ACT>
+void launch_persist(const GemmArgs &g, hipStream_t s, int blocks_per_cu) {
+  const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+  constexpr int smem = STAGES * (BM + BN) * 128;
+  static bool configured = false;
+  if (!configured) {
+    set_smem(gemm_persist_kernel<T, BM, BN, WM, WN, STAGES, ACT>, smem);
+    configured = true;
+  }
+  const int grid = std::min(tm * tn, 256 * blocks_per_cu);
+  hipLaunchKernelGGL((gemm_persist_kernel<T, BM, BN, WM, WN, STAGES, ACT>), dim3(grid), dim3(64 * WM * WN), smem, s,
+                     g, tm, tn);
+}
+
 template <typename T, int ACT>
 void launch_reg(const GemmArgs &g, hipStream_t s) {
   const int tm = (g.M + 127) / 128, tn = (g.N + 127) / 128;
@@ -441,10 +584,10 @@ constexpr int CUS = 256;
 int pick_tile(const GemmArgs &g) {
   const char *e = getenv("KH_GEMM_TILE");
   const int forced = e ? atoi(e) : -1;
-  if (forced >= 0 && forced <= 4) return forced;
-  auto blocks = [&](int bm, int bn) { return (int64_t)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * g.batch; };
-  if (blocks(256, 256) >= 2 * CUS) return 0;
-  if (blocks(256, 128) >= 2 * CUS) return 1;
+  if (forced >= 0 && forced <= 7) return forced;
+  // measured on MI355X (f16, random data): 128x128 with two blocks per CU leads on the ragged-batch
+  // shapes (M ~ 13k); the persistent 256x256 kernel leads once M is large and N wide
+  if (g.batch == 1 && g.M >= 65536 && g.N >= 1024) return 6;
   return 3;
 }
 
@@ -454,7 +597,12 @@ void launch_act(const GemmArgs &g, hipStream_t s) {
     launch_reg<T, ACT>(g, s);
     return;
   }
-  switch (pick_tile(g)) {
+  int cfg = pick_tile(g);
+  if (cfg >= 5 && g.batch > 1) cfg = 3;  // the persistent kernels walk one matrix
+  switch (cfg) {
+    case 5: launch_persist<T, 128, 128, 2, 2, 2, ACT>(g, s, 2); break;
+    case 6: launch_persist<T, 256, 256, 2, 4, 2, ACT>(g, s, 1); break;
+    case 7: launch_persist<T, 128, 128, 2, 2, 3, ACT>(g, s, 1); break;
     case 0: launch_dma<T, 256, 256, 2, 4, 2, ACT>(g, s); break;
     case 1: launch_dma<T, 256, 128, 2, 2, 3, ACT>(g, s); break;
     case 2: launch_dma<T, 128, 128, 2, 2, 4, ACT>(g, s); break;

@@ -12,15 +12,15 @@ enum Act : int { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2, ACT_TANH = 3, ACT_SIL
 
 // C[M, N] = act(A[M, K] W[N, K]^T + bias[N]); row strides lda, ldw, ldc in elements.
 struct GemmArgs {
-  const void *a;
-  int64_t lda;
-  const void *w;
-  int64_t ldw;
-  const void *bias;  // may be null
-  void *c;
-  int64_t ldc;
-  int M, N, K;
-  int act;
+  const void *a = nullptr;
+  int64_t lda = 0;
+  const void *w = nullptr;
+  int64_t ldw = 0;
+  const void *bias = nullptr;  // may be null
+  void *c = nullptr;
+  int64_t ldc = 0;
+  int M = 0, N = 0, K = 0;
+  int act = 0;
   // batched over z: pointer offsets (elements) per z index
   int batch = 1;
   int64_t a_bs = 0, w_bs = 0, c_bs = 0;
@@ -43,16 +43,16 @@ struct Packing {
 };
 
 struct EmbLnArgs {
-  const void *word;        // packed word rows [T, N], or null with table + ids
-  const void *table;       // device word table [rows, N]
-  const int32_t *ids;      // packed ids [T]
-  const void *pos;         // [maxpos, N] or null (zero table)
-  const void *typ;         // [types, N] or null (zero table)
-  const uint32_t *tt;      // packed type ids [T] or null
-  const void *gamma, *beta;
-  void *out;
-  int N, offset, maxpos, posids;
-  float eps;
+  const void *word = nullptr;    // packed word rows [T, N], or null with table + ids
+  const void *table = nullptr;   // device word table [rows, N]
+  const int32_t *ids = nullptr;  // packed ids [T]
+  const void *pos = nullptr;     // [maxpos, N] or null (zero table)
+  const void *typ = nullptr;     // [types, N] or null (zero table)
+  const uint32_t *tt = nullptr;  // packed type ids [T] or null
+  const void *gamma = nullptr, *beta = nullptr;
+  void *out = nullptr;
+  int N = 0, offset = 0, maxpos = 1, posids = 0;
+  float eps = 0.f;
 };
 void embln(bool f16, const EmbLnArgs &a, const Packing &p, hipStream_t s);
 
@@ -79,11 +79,11 @@ void gather_rows(bool f16, const void *x, const uint32_t *markers, void *states,
 // Standard attention over packed rows: ctx = softmax(scale q k^T, window) v per (sequence, head).
 // tiles: [ntiles] (sequence, first query) pairs of 64-query tiles.
 struct AttnArgs {
-  const void *qkv;   // [T, 3 H D]
-  void *ctx;         // [T, H D]
-  int H, D;
-  float scale;       // multiplies q.k (standard) ...
-  int window;        // 0: global, else |i - j| <= window
+  const void *qkv = nullptr;  // [T, 3 H D]
+  void *ctx = nullptr;        // [T, H D]
+  int H = 0, D = 0;
+  float scale = 1.f;          // multiplies the score
+  int window = 0;             // 0: global, else |i - j| <= window
   // DeBERTa relative terms: score = (q.k + c2p[i][h][bucket] + p2c[j][h][bucket]) * scale
   const float *c2p = nullptr;  // [T, H, NB]
   const float *p2c = nullptr;  // [T, H, NB]

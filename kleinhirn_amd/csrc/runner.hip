@@ -585,6 +585,7 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
         g.w_bs = s.D;
         g.c_bs = nb;
         g.c_f32 = true;
+        g.bias = nullptr;
         g.a = a.qkv;
         g.w = bufp(pl, s.in[2]);
         g.c = pl->d_c2p.p;
