@@ -245,25 +245,40 @@ gemm_dma_kernel(GemmArgs g, int tiles_m, int tiles_n) {
     }
     if (it + STAGES - 1 < nk) issue((it + STAGES - 1) % STAGES, (it + STAGES - 1) * BK);
     const char *slab = smem + (it % STAGES) * STAGE;
-    // every fragment read of the slab is issued first; LDS answers in order, so the MFMAs of step
-    // kk wait only for the reads of step kk (partial lgkmcnt waits)
     constexpr int KK = BK / MF::KSTEP;
-    typename MF::frag af[KK][FM], bf[KK][FN];
+    typename MF::frag af[2][FM], bf[2][FN];
+    auto rd = [&](int kk, int s) {
+#pragma unroll
+      for (int i = 0; i < FM; i++) af[s][i] = MF::lds(slab, arow + i * 32, kk, lg);
+#pragma unroll
+      for (int j = 0; j < FN; j++) bf[s][j] = MF::lds(slab, brow + j * 32, kk, lg);
+    };
+    // the MFMA phase outranks the other block's epilogue (VALU) on this CU
+    __builtin_amdgcn_s_setprio(1);
+    rd(0, 0);
 #pragma unroll
     for (int kk = 0; kk < KK; kk++) {
-#pragma unroll
-      for (int i = 0; i < FM; i++) af[kk][i] = MF::lds(slab, arow + i * 32, kk, lg);
-#pragma unroll
-      for (int j = 0; j < FN; j++) bf[kk][j] = MF::lds(slab, brow + j * 32, kk, lg);
-    }
-    __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
-#pragma unroll
-    for (int kk = 0; kk < KK; kk++)
+      if (kk + 1 < KK) rd(kk + 1, (kk + 1) & 1);
 #pragma unroll
       for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < FN; j++) acc[i][j] = MF::mma(af[kk][i], bf[kk][j], acc[i][j]);
+        for (int j = 0; j < FN; j++) acc[i][j] = MF::mma(af[kk & 1][i], bf[kk & 1][j], acc[i][j]);
+    }
+    // schedule: DMA issue, reads of step 0, then the reads of step kk + 1 spread between the MFMAs
+    // of step kk
+    __builtin_amdgcn_sched_group_barrier(0x020, P, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);
+#pragma unroll
+    for (int kk = 0; kk < KK - 1; kk++) {
+#pragma unroll
+      for (int r = 0; r < FM + FN; r++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, (FM * FN + FM + FN - 1) / (FM + FN), 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);
   }
+  __builtin_amdgcn_s_setprio(0);
   if constexpr (sizeof(T) == 2) {
     if (!g.c_f32 && g.N % 8 == 0 && g.ldc % 8 == 0) {
       epilogue_lds<BM, BN, WM, WN, ACT>(g, acc, m0, n0, wm, wn, lane, z, smem);

@@ -25,8 +25,7 @@ struct GemmArgs {
   int batch = 1;
   int64_t a_bs = 0, w_bs = 0, c_bs = 0;
   bool c_f32 = false;  // write f32 output whatever the storage type (relative-position scores)
-  // one wavefront per output group: pooled-head steps, so a sequence's result does not depend on
-  // how many sequences share the batch
+  // force the wavefront-per-output kernel (tests)
   bool rowdot = false;
 };
 void gemm(bool f16, const GemmArgs &g, hipStream_t s);

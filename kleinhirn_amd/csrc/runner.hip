@@ -489,7 +489,6 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
       g.N = s.N;
       g.K = s.K;
       g.act = s.act;
-      g.rowdot = s.seq_rows;
       begin(gemm_uses_mfma(f16, g) ? "gemm_mfma" : "gemm_rowdot", 2.0 * rows * s.N * s.K,
             (double)es * ((double)rows * s.K + (double)s.N * s.K + (double)rows * s.N + (g.bias ? s.N : 0)));
       gemm(f16, g, st);

@@ -808,6 +808,10 @@ int kho_run(const kho_op *ops, int nops, int L, int batch, const float *mask, in
 }
 
 /* exported single kernels for the closed-form tests */
+void kho_softmax_row(float *p, int n, const float *mask, int first, int il, int window, int qmask, int dense,
+                     float scale) {
+  softmax_row(p, n, mask, first, il, window, qmask, dense, scale);
+}
 float kho_vexp(float x) { return vexp1(x); }
 float kho_vgelu(float x) { return vgelu1(x); }
 float kho_gelu(float x) { return gelu_m(x); }

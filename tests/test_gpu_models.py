@@ -7,6 +7,8 @@ every decision f16 rounding cannot flip (top-2 gap >= 2 delta, convert/k28_close
 Sequences are subsets of the benchmark batches so the oracle finishes in seconds."""
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -27,11 +29,22 @@ CASES = {
 _cache: dict = {}
 
 
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
 def case_and_oracle(key):
+    """The seeded case and the oracle's outputs for it: the committed golden vectors (made by
+    tests/golden/make_golden.py from the same case), and for c2 also a live oracle run."""
     if key not in _cache:
         w, batch, layers, length, max_len = CASES[key]
         case = workload_case(w, batch, layers, length, max_len)
-        _cache[key] = (case, oracle_outputs(case))
+        g = np.load(os.path.join(GOLDEN, f"oracle_{key}.npz"))
+        assert np.array_equal(np.concatenate(case.ids).astype(np.int32), g["ids"]), "golden ids differ from the case"
+        ref = g["out"]
+        if key == "c2":
+            live = oracle_outputs(case)
+            assert np.allclose(live, ref, rtol=0, atol=1e-6)
+        _cache[key] = (case, ref)
     return _cache[key]
 
 
