@@ -41,7 +41,22 @@ def build(verbose: bool = False) -> str:
     tmp = LIB + ".tmp"
     subprocess.run([HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", *objs, "-o", tmp], check=True)
     os.replace(tmp, LIB)
+    build_addon()
     return LIB
+
+
+ADDON = os.path.join(HERE, "node", "kh_addon.node")
+NODE_INCLUDE = "/usr/include/node"
+
+
+def build_addon() -> str | None:
+    """kh_addon.node (plain N-API C) against libkh_hip.so, when the Node headers are present."""
+    if not os.path.exists(os.path.join(NODE_INCLUDE, "node_api.h")):
+        return None
+    subprocess.run(["gcc", "-O2", "-shared", "-fPIC", "-std=c11", "-Wall", f"-I{NODE_INCLUDE}",
+                    "-DNODE_GYP_MODULE_NAME=kh_addon", os.path.join(HERE, "node", "kh_addon.c"),
+                    "-o", ADDON, f"-L{HERE}", "-lkh_hip", "-Wl,-rpath,$ORIGIN/.."], check=True)
+    return ADDON
 
 
 if __name__ == "__main__":

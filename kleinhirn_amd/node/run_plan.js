@@ -1,0 +1,39 @@
+// Runs one exported plan through kh_addon.node the way hip-backend.ts drives it (weights, check,
+// runner with init tables, upload, run, asynchronous readback) and writes the f32 output.
+//   node run_plan.js <case dir>       (files written by kleinhirn_amd.node_case.export_case)
+'use strict';
+const fs = require('fs');
+const path = require('path');
+
+const dir = process.argv[2];
+const addon = require(process.env.KH_ADDON || path.join(__dirname, 'kh_addon.node'));
+const read = (f) => fs.readFileSync(path.join(dir, f));
+const meta = JSON.parse(read('meta.json'));
+const planText = read('plan.json').toString();
+const typed = (buf, Ctor) => new Ctor(buf.buffer, buf.byteOffset, buf.byteLength / Ctor.BYTES_PER_ELEMENT);
+
+if (meta.checkOnly) {
+  addon.planCheck(null, planText);
+  console.log(JSON.stringify({ ok: true }));
+  process.exit(0);
+}
+
+(async () => {
+  const ctx = addon.ctxCreate(0);
+  for (const w of meta.weights) addon.weightAdd(ctx, w.name, w.dtype, w.shape, read(w.file));
+  addon.planCheck(ctx, planText);
+  const plan = addon.planCreate(ctx, planText);
+  for (const [id, file] of Object.entries(meta.inits)) addon.planInitBuffer(plan, id, read(file));
+  const emb = read('emb.bin');
+  const tt = meta.typeIds ? typed(read('tt.bin'), Uint32Array) : null;
+  addon.upload(plan, emb, typed(read('mask.bin'), Float32Array), tt);
+  addon.run(plan, meta.rows);
+  const out = await addon.readOutputAsync(plan);
+  fs.writeFileSync(path.join(dir, 'out.bin'), Buffer.from(out.buffer, out.byteOffset, out.byteLength));
+  console.log(JSON.stringify({ ok: true, n: out.length, ms: addon.lastRunMs(plan), info: addon.planInfo(plan) }));
+  addon.planDestroy(plan);
+  addon.ctxDestroy(ctx);
+})().catch((e) => {
+  console.error(e.message);
+  process.exit(1);
+});

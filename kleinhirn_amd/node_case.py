@@ -1,0 +1,49 @@
+"""Exports a plan, its weights and one RunInput as files for kleinhirn_amd/node/run_plan.js, so the
+Node-API path (the host side hip-backend.ts uses) runs the same case as the Python host."""
+from __future__ import annotations
+
+import json
+import os
+import subprocess
+
+import numpy as np
+
+from .plan.build import plan_inits, plan_json
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ADDON = os.path.join(HERE, "node", "kh_addon.node")
+RUNNER = os.path.join(HERE, "node", "run_plan.js")
+
+
+def export_case(dirname: str, plan: dict, weights: dict | None = None, run_input: dict | None = None,
+                rows: int | None = None, check_only: bool = False) -> None:
+    os.makedirs(dirname, exist_ok=True)
+    with open(os.path.join(dirname, "plan.json"), "w") as f:
+        json.dump(plan_json(plan), f)
+    meta = {"checkOnly": check_only, "weights": [], "inits": {}, "rows": rows or 0,
+            "typeIds": bool(run_input is not None and run_input.get("typeIds") is not None)}
+    if not check_only:
+        for i, (name, t) in enumerate(weights.items()):
+            t = np.ascontiguousarray(t)
+            fn = f"w{i}.bin"
+            t.tofile(os.path.join(dirname, fn))
+            meta["weights"].append({"name": name, "dtype": 1 if t.dtype == np.float16 else 0,
+                                    "shape": list(t.shape), "file": fn})
+        for i, (bid, raw) in enumerate(plan_inits(plan).items()):
+            fn = f"init{i}.bin"
+            with open(os.path.join(dirname, fn), "wb") as f:
+                f.write(raw)
+            meta["inits"][bid] = fn
+        np.ascontiguousarray(run_input["embeddings"]).tofile(os.path.join(dirname, "emb.bin"))
+        np.ascontiguousarray(run_input["mask"], dtype=np.float32).tofile(os.path.join(dirname, "mask.bin"))
+        if meta["typeIds"]:
+            np.ascontiguousarray(run_input["typeIds"], dtype=np.uint32).tofile(os.path.join(dirname, "tt.bin"))
+    with open(os.path.join(dirname, "meta.json"), "w") as f:
+        json.dump(meta, f)
+
+
+def run_node(dirname: str, timeout: int = 120) -> dict:
+    r = subprocess.run(["node", RUNNER, dirname], capture_output=True, text=True, timeout=timeout)
+    if r.returncode != 0:
+        raise RuntimeError(f"node run_plan.js failed: {r.stderr.strip()}")
+    return json.loads(r.stdout.strip().splitlines()[-1])

@@ -1,0 +1,214 @@
+// HIP backend: the Backend / PlanRunner seam (src/backend.ts:74-106 of kleinhirn) on one MI355X
+// through libkh_hip.so (include/kh_hip.h) and its Node-API binding kh_addon.node. Drop-in beside
+// src/webgpu-backend.ts and src/wasm-backend.ts: the plans of src/plan/build.ts run unchanged; the
+// library stores each plan's rows packed (cu_seqlens from the prefix mask) and computes only the
+// valid rows on hand-written gfx950 kernels.
+//
+// Node only (a native addon). Integration in the host repository:
+//   * widen Backend.kind in src/backend.ts to 'webgpu' | 'wasm' | 'hip';
+//   * let loadBackend (src/backend.ts:135-149) call loadHip when asked for the HIP backend.
+// EncoderModel needs no change: one call in flight per model (src/encoder.ts:265-269) matches the
+// library's one-stream-per-plan contract.
+
+import { createRequire } from 'node:module';
+import type { Backend, LoadedBackend, PlanRunner } from './backend.ts';
+import type { RunInput } from './plan/executor.ts';
+import type { Plan } from './plan/ir.ts';
+import { fetchShardBytes, loadWords, type Manifest } from './weights.ts';
+import type { WordsFetch } from './words.ts';
+
+// The addon's surface (kleinhirn_amd/node/kh_addon.c); handles are opaque.
+export type KhHandle = { readonly __kh: unique symbol };
+export interface KhAddon {
+  abiVersion(): number;
+  ctxCreate(device: number): KhHandle;
+  ctxDestroy(ctx: KhHandle): void;
+  weightAdd(ctx: KhHandle, name: string, dtype: number, shape: number[], data: ArrayBufferView): void;
+  weightBytes(ctx: KhHandle): number;
+  wordsSet(ctx: KhHandle, dtype: number, rows: number, width: number, data: ArrayBufferView): void;
+  planCheck(ctx: KhHandle | null, json: string): void;
+  planCreate(ctx: KhHandle, json: string): KhHandle;
+  planInitBuffer(plan: KhHandle, id: string, data: ArrayBufferView): void;
+  planInfo(plan: KhHandle): { length: number; batch: number; markers: number; f16: number; bytes: number;
+    outRows: number; outCols: number; launches: number };
+  planDestroy(plan: KhHandle): void;
+  upload(plan: KhHandle, embeddings: ArrayBufferView, mask: Float32Array, typeIds: Uint32Array | null): void;
+  uploadIds(plan: KhHandle, ids: Int32Array, mask: Float32Array, typeIds: Uint32Array | null): void;
+  run(plan: KhHandle, rows: number): void;
+  readOutput(plan: KhHandle): Float32Array;
+  readOutputAsync(plan: KhHandle): Promise<Float32Array>;
+  lastRunMs(plan: KhHandle): number;
+}
+
+const KH_F32 = 0;
+const KH_F16 = 1;
+const ABI = 1;
+
+export function loadAddon(path?: string): KhAddon {
+  const req = createRequire(import.meta.url);
+  const addon = req(path ?? process.env.KH_ADDON ?? 'kh_addon.node') as KhAddon;
+  if (addon.abiVersion() !== ABI) throw new Error(`kh_addon ABI ${addon.abiVersion()}, expected ${ABI}`);
+  return addon;
+}
+
+// The plan as the library reads it: the typed-array init tables travel through planInitBuffer.
+export function planJson(plan: Plan): string {
+  return JSON.stringify(plan, (key, value) => (key === 'init' ? undefined : value));
+}
+
+export class HipPlanRunner implements PlanRunner {
+  readonly length: number;
+  readonly batch: number;
+  readonly markers: number;
+  private h: KhHandle | undefined;
+
+  constructor(private kh: KhAddon, ctx: KhHandle, private plan: Plan) {
+    this.length = plan.length;
+    this.batch = plan.batch;
+    this.markers = plan.markers;
+    const h = kh.planCreate(ctx, planJson(plan));
+    try {
+      for (const b of plan.buffers) if (b.init) kh.planInitBuffer(h, b.id, b.init);
+    } catch (e) {
+      kh.planDestroy(h);
+      throw e;
+    }
+    this.h = h;
+  }
+
+  private handle(): KhHandle {
+    if (!this.h) throw new Error('HIP plan runner used after destroy');
+    return this.h;
+  }
+
+  get bytes(): number {
+    return this.kh.planInfo(this.handle()).bytes;
+  }
+
+  upload(input: RunInput): void {
+    if (input.packedMarkers) throw new Error('marker inputs (GLiNER, Julia) are outside the HIP encoder heads');
+    if (this.plan.inputs.typeIds && !input.typeIds) throw new Error('plan needs typeIds');
+    this.kh.upload(this.handle(), input.embeddings, input.mask, input.typeIds ?? null);
+  }
+
+  run(seqLen: number, capture?: boolean): void {
+    if (capture) this.assertCapturable();
+    this.kh.run(this.handle(), seqLen);
+  }
+
+  readOutput(): Promise<Float32Array> {
+    return this.kh.readOutputAsync(this.handle());
+  }
+
+  readCapture(): Promise<Float32Array> {
+    return Promise.reject(new Error('capture is the WebGPU f32 parity tool; the HIP runner has none'));
+  }
+
+  assertCapturable(): void {
+    throw new Error('capture is the WebGPU f32 parity tool; the HIP runner has none');
+  }
+
+  // GPU milliseconds of the last run (hipEvents on the plan's stream)
+  lastRunMs(): number {
+    return this.kh.lastRunMs(this.handle());
+  }
+
+  destroy(): void {
+    if (this.h) this.kh.planDestroy(this.h);
+    this.h = undefined;
+  }
+}
+
+export class HipBackend implements Backend {
+  // Backend.kind is 'webgpu' | 'wasm' in src/backend.ts:91; the HIP seam widens it
+  readonly kind = 'hip' as unknown as 'wasm';
+  private ctx: KhHandle | undefined;
+
+  constructor(private kh: KhAddon, device = 0) {
+    this.ctx = kh.ctxCreate(device);
+  }
+
+  private context(): KhHandle {
+    if (!this.ctx) throw new Error('HIP backend used after dispose');
+    return this.ctx;
+  }
+
+  get weightBytes(): number {
+    return this.kh.weightBytes(this.context());
+  }
+
+  addTensor(name: string, dtype: string, shape: number[], bytes: Uint8Array): void {
+    if (dtype !== 'f16' && dtype !== 'f32') throw new Error(`tensor ${name}: dtype ${dtype}`);
+    this.kh.weightAdd(this.context(), name, dtype === 'f16' ? KH_F16 : KH_F32, shape, bytes);
+  }
+
+  // Device-resident word table: runs by token id gather rows on the GPU (kh_upload_ids).
+  setWords(dtype: 'f16' | 'f32', rows: number, width: number, bytes: Uint8Array): void {
+    this.kh.wordsSet(this.context(), dtype === 'f16' ? KH_F16 : KH_F32, rows, width, bytes);
+  }
+
+  check(plan: Plan): void {
+    this.kh.planCheck(this.context(), planJson(plan));
+  }
+
+  runner(plan: Plan): PlanRunner {
+    return new HipPlanRunner(this.kh, this.context(), plan);
+  }
+
+  // A packed plan holds any batch that fits HBM: the asked size is the fitting size.
+  fitBatch(build: (batch: number) => Plan, batch: number): Plan | undefined {
+    return batch > 1 ? build(batch) : undefined;
+  }
+
+  async prepare<S>(work: () => S): Promise<S> {
+    return work();
+  }
+
+  call<S, R>(start: () => S, read: (started: S) => Promise<R>): Promise<R> {
+    let started: S;
+    try {
+      started = start();
+    } catch (e) {
+      return Promise.reject(e);
+    }
+    return read(started);
+  }
+
+  info(): Record<string, unknown> {
+    return { backend: 'hip', weightBytes: this.weightBytes, abi: this.kh.abiVersion() };
+  }
+
+  dispose(): void {
+    if (this.ctx) this.kh.ctxDestroy(this.ctx);
+    this.ctx = undefined;
+  }
+}
+
+// Weights of a manifest into one HIP context (the loadGpu of src/webgpu-backend.ts:104-108 for HIP):
+// every tensor except the word table, which stays on the host as in the other backends.
+export async function loadHip(
+  manifestUrl: string, manifest: Manifest, started?: Promise<WordsFetch>,
+  options: { device?: number; addon?: KhAddon } = {},
+): Promise<LoadedBackend> {
+  const kh = options.addon ?? loadAddon();
+  const fetched = await fetchShardBytes(manifestUrl, manifest);
+  const backend = new HipBackend(kh, options.device ?? 0);
+  const tUp = performance.now();
+  try {
+    for (const t of fetched.manifest.tensors) {
+      if (t.keepOnCpu) continue;
+      backend.addTensor(t.name, t.dtype, t.shape, new Uint8Array(fetched.shardBytes[t.shard], t.offset, t.byteLength));
+    }
+  } catch (e) {
+    backend.dispose();
+    throw e;
+  }
+  const uploadMs = performance.now() - tUp;
+  const base = manifestUrl.slice(0, manifestUrl.lastIndexOf('/') + 1);
+  const words = await loadWords(base, fetched.manifest, fetched.shardBytes, started);
+  return {
+    backend, words: words.table, downloadBytes: fetched.downloadBytes + words.bytes,
+    timing: { fetchMs: fetched.fetchMs, bodyMs: fetched.bodyMs, sha256Ms: fetched.sha256Ms, uploadMs,
+      ...words.timing },
+  };
+}

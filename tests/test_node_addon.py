@@ -1,0 +1,55 @@
+"""The Node-API path hip-backend.ts uses (kh_addon.node over libkh_hip.so), driven by
+kleinhirn_amd/node/run_plan.js: structural plan checks on the CPU, and on the GPU the same case as
+the Python host, compared bit for bit and against the golden oracle vectors."""
+from __future__ import annotations
+
+import os
+import shutil
+import tempfile
+
+import numpy as np
+import pytest
+
+from kleinhirn_amd import configs, inputs
+from kleinhirn_amd.node_case import ADDON, export_case, run_node
+from kleinhirn_amd.plan.build import build_plan
+
+pytestmark = pytest.mark.skipif(shutil.which("node") is None or not os.path.exists(ADDON),
+                                reason="node or kh_addon.node missing")
+
+
+def test_node_addon_checks_every_benchmark_plan():
+    for name in ("c2", "c3b", "c4"):
+        w = configs.ALL[name]()
+        with tempfile.TemporaryDirectory() as d:
+            export_case(d, build_plan(w.spec, w.head, w.length, 16, True), check_only=True)
+            assert run_node(d)["ok"]
+
+
+def test_node_addon_reports_unsupported_ops():
+    w = configs.c2()
+    plan = build_plan(w.spec, w.head, 64, 1, True)
+    plan["segments"][0]["ops"][0]["kernel"] = "im2col"
+    with tempfile.TemporaryDirectory() as d:
+        export_case(d, plan, check_only=True)
+        with pytest.raises(RuntimeError, match="im2col"):
+            run_node(d)
+
+
+@pytest.mark.gpu
+def test_node_path_matches_python_path_and_golden():
+    from tests.helpers import decision_parity, hip_outputs
+    from tests.test_gpu_models import case_and_oracle
+    case, ref = case_and_oracle("c2")
+    W = configs.storage(case.weights, True)
+    plan = build_plan(case.spec, case.head, case.length, len(case.ids), True)
+    ri = inputs.run_input(case.spec, W["embeddings.word.weight"], case.ids, case.length)
+    with tempfile.TemporaryDirectory() as d:
+        export_case(d, plan, W, ri, rows=case.length * len(case.ids))
+        res = run_node(d)
+        got = np.fromfile(os.path.join(d, "out.bin"), dtype=np.float32).reshape(len(case.ids), -1)
+    assert res["ok"] and res["info"]["launches"] > 0
+    py = hip_outputs(case, f16=True)
+    assert np.array_equal(got, py)
+    d = decision_parity(ref, got)
+    assert d["mismatched"] == 0, d
