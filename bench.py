@@ -24,6 +24,16 @@ sys.path.insert(0, ROOT)
 
 PEAK = {"f16_mfma_tflops": 2500.0, "f32_mfma_tflops": 157.3, "hbm_gbs": 8000.0}
 
+# HBM bytes per launch of a workload's dominant kernel family, from two rocprofv3 --pmc runs of this
+# bench (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch averaged over the family), each counter scaled
+# by what it reads for a plain device copy of 1 GiB (python3 -m kleinhirn_amd.profiling copy 1024:
+# FETCH_SIZE reads 0.5 GiB -> x2.0, WRITE_SIZE reads 1.0 GiB -> x1.0). Summaries with the commands:
+# profiles/gemm_mfma_c2_roberta_base_ragged256_traffic.md. Re-measured whenever the kernel changes.
+FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
+TRAFFIC_KIB = {  # (workload, family): (FETCH_SIZE KiB, WRITE_SIZE KiB) per dispatch
+    ("c2-roberta-base-f16-ragged256", "gemm_mfma"): (68756.3, 42329.5),
+}
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -149,9 +159,13 @@ def main() -> int:
         achieved = dom["bytes"] / dom["launches"] / (avg_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK["hbm_gbs"], "unit": "GB/s"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    roof["traffic"] = None
+    kib = TRAFFIC_KIB.get((w.name, dom_name))
+    roof["traffic"] = round((kib[0] * FETCH_SCALE + kib[1] * WRITE_SCALE) * 1024) if kib else None
+    roof["traffic_unit"] = "bytes/launch (rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE, copy-calibrated)"
+    roof["algorithmic_bytes"] = round(dom["bytes"] / dom["launches"])
     roof["kernel"] = dom_name
     roof["avg_launch_ms"] = round(avg_ms, 4)
+    roof["launches"] = dom["launches"]
 
     cpu = None
     if not args.no_cpu:
