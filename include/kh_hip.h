@@ -57,19 +57,19 @@ int kh_ctx_destroy(kh_ctx *ctx);
 int kh_weight_add(kh_ctx *ctx, const char *name, int dtype, const int64_t *shape, int ndim,
                   const void *data, size_t bytes);
 
-/* Bytes of the loaded weights in device memory (Backend.weightBytes, src/backend.ts:92-93). */
+/* Bytes of the loaded weights in device memory (Backend.weightBytes, src/backend.ts:32-33). */
 int kh_ctx_weight_bytes(const kh_ctx *ctx, uint64_t *out);
 
 /* Optional device-resident word table [rows, width] in `dtype` (the step before the plan: the
  * reference gathers word rows on the host, src/encoder.ts:271-282); enables kh_upload_ids. */
 int kh_words_set(kh_ctx *ctx, int dtype, int64_t rows, int64_t width, const void *data, size_t bytes);
 
-/* Backend.check (src/backend.ts:94-95): KH_OK when the plan (JSON of the reference's Plan, typed
+/* Backend.check (src/backend.ts:34-35): KH_OK when the plan (JSON of the reference's Plan, typed
  * `init` tables left out) can run here, else an error naming every op that cannot. With a null
  * context only the plan's structure is checked (no weights, no device needed). */
 int kh_plan_check(kh_ctx *ctx, const char *plan_json, size_t len);
 
-/* Backend.runner (src/backend.ts:96, src/plan/executor.ts:85-99): builds every buffer and the
+/* Backend.runner (src/backend.ts:36, src/plan/executor.ts:85-99): builds every buffer and the
  * launch list up front. */
 int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out);
 
@@ -102,11 +102,11 @@ int kh_upload(kh_plan *plan, const void *emb, size_t emb_bytes, const float *mas
 int kh_upload_ids(kh_plan *plan, const int32_t *ids, size_t id_count, const float *mask,
                   size_t mask_count, const uint32_t *type_ids, size_t type_count);
 
-/* PlanRunner.run (src/plan/executor.ts:294-297): one forward over `rows` rows (the real rows of
+/* PlanRunner.run (src/plan/executor.ts:295-297): one forward over `rows` rows (the real rows of
  * a B = 1 call, L * B for a batch plan), enqueued on the plan's stream; returns without waiting. */
 int kh_run(kh_plan *plan, int32_t rows);
 
-/* PlanRunner.readOutput (src/plan/executor.ts:395-408): waits, then writes rows * cols f32
+/* PlanRunner.readOutput (src/plan/executor.ts:398-408): waits, then writes rows * cols f32
  * values (f16 storage converted) in the plan's output layout. */
 int kh_read_output(kh_plan *plan, float *out, size_t count);
 

@@ -1,4 +1,4 @@
-// HIP backend: the Backend / PlanRunner seam (src/backend.ts:74-106 of kleinhirn) on one MI355X
+// HIP backend: the Backend / PlanRunner seam (src/backend.ts:14-46 of kleinhirn) on one MI355X
 // through libkh_hip.so (include/kh_hip.h) and its Node-API binding kh_addon.node. Drop-in beside
 // src/webgpu-backend.ts and src/wasm-backend.ts: the plans of src/plan/build.ts run unchanged; the
 // library stores each plan's rows packed (cu_seqlens from the prefix mask) and computes only the
@@ -6,8 +6,8 @@
 //
 // Node only (a native addon). Integration in the host repository:
 //   * widen Backend.kind in src/backend.ts to 'webgpu' | 'wasm' | 'hip';
-//   * let loadBackend (src/backend.ts:135-149) call loadHip when asked for the HIP backend.
-// EncoderModel needs no change: one call in flight per model (src/encoder.ts:265-269) matches the
+//   * let loadBackend (src/backend.ts:75-89) call loadHip when asked for the HIP backend.
+// EncoderModel needs no change: one call in flight per model (src/encoder.ts:5-8) matches the
 // library's one-stream-per-plan contract.
 
 import { createRequire } from 'node:module';
@@ -120,7 +120,7 @@ export class HipPlanRunner implements PlanRunner {
 }
 
 export class HipBackend implements Backend {
-  // Backend.kind is 'webgpu' | 'wasm' in src/backend.ts:91; the HIP seam widens it
+  // Backend.kind is 'webgpu' | 'wasm' in src/backend.ts:31; the HIP seam widens it
   readonly kind = 'hip' as unknown as 'wasm';
   private ctx: KhHandle | undefined;
 
@@ -184,7 +184,7 @@ export class HipBackend implements Backend {
   }
 }
 
-// Weights of a manifest into one HIP context (the loadGpu of src/webgpu-backend.ts:104-108 for HIP):
+// Weights of a manifest into one HIP context (the loadGpu of src/webgpu-backend.ts:103 for HIP):
 // every tensor except the word table, which stays on the host as in the other backends.
 export async function loadHip(
   manifestUrl: string, manifest: Manifest, started?: Promise<WordsFetch>,
