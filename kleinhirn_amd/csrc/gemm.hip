@@ -10,9 +10,9 @@
 // 16 bytes land at LDS base + 16 * lane, no VGPR staging) into a ring of STAGES slabs of 128-byte
 // rows (64 halves / 32 floats of k). The loads of slab i + STAGES - 1 are issued while slab i feeds
 // the MFMAs, so STAGES - 1 slabs of every operand are in flight per CU; one barrier per slab.
-// The 16-byte chunks of each row are XOR-swizzled by row (chunk c of row r sits at c ^ (r & 7)):
+// The 16-byte chunks of each row are XOR-swizzled by row (chunk c of row r sits at c ^ swz(r)):
 // the lanes of one load instruction fetch the chunks in swizzled order, and the fragment reads of
-// 8 consecutive rows hit 8 different bank groups.
+// 16 consecutive rows hit 16 different bank groups.
 //
 // Larger wavefront tiles cut LDS traffic per MFMA (a 64 x 64 wavefront tile needs the full LDS
 // bandwidth at the MFMA rate, 128 x 64 needs 3/4 of it); smaller block tiles keep more CUs busy on
@@ -28,6 +28,7 @@
 // products (head steps with a handful of classes) to one wavefront per (row, 4 columns).
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "kernels.h"
 #include "device.h"
@@ -39,6 +40,11 @@ namespace {
 typedef __attribute__((address_space(3))) void lds_void;
 typedef const __attribute__((address_space(1))) void gbl_void;
 
+// LDS swizzle of 128-byte slab rows: chunk c of row r sits at c ^ swz(r). The LDS serves 256 bytes
+// (64 banks) per cycle, two 128-byte rows; with this key any 16 consecutive rows read at one
+// chunk land in 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+
 template <typename T>
 struct Mfma;
 
@@ -48,7 +54,7 @@ struct Mfma<half_t> {
   static constexpr int KSTEP = 16;   // k per MFMA
   typedef half8v frag;
   __device__ static frag lds(const char *slab, int row, int kk, int g) {
-    const int chunk = (kk * 2 + g) ^ (row & 7);
+    const int chunk = (kk * 2 + g) ^ swz(row);
     return *reinterpret_cast<const half8v *>(slab + row * 128 + chunk * 16);
   }
   __device__ static float16v mma(frag a, frag b, float16v c) {
@@ -63,7 +69,7 @@ struct Mfma<float> {
   typedef float frag;
   __device__ static frag lds(const char *slab, int row, int kk, int g) {
     const int k = kk * 2 + g;
-    const int chunk = (k >> 2) ^ (row & 7);
+    const int chunk = (k >> 2) ^ swz(row);
     return *reinterpret_cast<const float *>(slab + row * 128 + chunk * 16 + (k & 3) * 4);
   }
   __device__ static float16v mma(frag a, frag b, float16v c) {
@@ -196,12 +202,13 @@ gemm_dma_kernel(GemmArgs g, int tiles_m, int tiles_n) {
   const int lg = lane >> 5;
 
   // this lane's source rows for its P load instructions (row clamped to the matrix)
-  const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+  const int lrow = lane >> 3;
   const T *src[P];
 #pragma unroll
   for (int p = 0; p < P; p++) {
     const int grp = wave * P + p;
     const int r = grp * 8 + lrow;  // row inside the A | W slab
+    const int lchunk = (lane & 7) ^ swz(r);
     if (r < BM) {
       const int m = m0 + r < g.M ? m0 + r : g.M - 1;
       src[p] = A + (int64_t)m * g.lda + lchunk * CE;
@@ -322,7 +329,7 @@ gemm_persist_kernel(GemmArgs g, int tiles_m, int tiles_n) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int lg = lane >> 5;
-  const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+  const int lrow = lane >> 3;
 
   auto tile_of = [&](int j, int &m0, int &n0) {
     const int t = xcd_tile(b + j * G, ntiles);
@@ -339,6 +346,7 @@ gemm_persist_kernel(GemmArgs g, int tiles_m, int tiles_n) {
     for (int p = 0; p < P; p++) {
       const int grp = wave * P + p;
       const int r = grp * 8 + lrow;
+      const int lchunk = (lane & 7) ^ swz(r);
       const T *src;
       if (r < BM) {
         const int m = m0 + r < g.M ? m0 + r : g.M - 1;
@@ -464,12 +472,12 @@ __global__ void __launch_bounds__(256) gemm_reg_kernel(GemmArgs g, int tiles_m, 
 #pragma unroll
     for (int i = 0; i < LA; i++) {
       const int q = t + i * NT, r = q >> 3, c = q & 7;
-      *reinterpret_cast<uint4 *>(sa + r * 128 + ((c ^ (r & 7)) << 4)) = ra[i];
+      *reinterpret_cast<uint4 *>(sa + r * 128 + ((c ^ swz(r)) << 4)) = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < LB; i++) {
       const int q = t + i * NT, r = q >> 3, c = q & 7;
-      *reinterpret_cast<uint4 *>(sb + r * 128 + ((c ^ (r & 7)) << 4)) = rb[i];
+      *reinterpret_cast<uint4 *>(sb + r * 128 + ((c ^ swz(r)) << 4)) = rb[i];
     }
   };
 
@@ -543,6 +551,170 @@ __global__ void __launch_bounds__(256) gemm_rowdot_kernel(GemmArgs g) {
   }
 }
 
+
+// Lean f16 kernel: the same slab ring as gemm_dma_kernel (two stages, direct-to-LDS loads,
+// swizzled 128-byte rows) with the per-tile and per-slab vector-ALU work cut down, since with two
+// blocks per CU every VALU slot competes with the other block's MFMAs:
+//  * loads go through buffer resources over the tile's row panels (rows past M / N read as zero),
+//    so a slab's k advance is one scalar offset and the LDS destination sits in M0;
+//  * fragment read addresses are computed once per tile (rows arow + 32 i share the swizzle of
+//    arow) and the loop is unrolled over the two stages, so every LDS read has a constant offset;
+//  * the first MFMA of a tile takes a zero accumulator instead of zeroed registers;
+//  * operands are swapped (D = W A^T per 32 x 32 tile), so a lane holds four consecutive output
+//    columns of one row: bias, activation and the f16 conversion run on 4-wide groups that land in
+//    LDS with one 8-byte write, and the block stores whole 16-byte row chunks.
+// Needs f16 storage, K % 64 == 0, N % 8 == 0 and ldc % 8 == 0; one matrix (batch 1).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t panel_rsrc(const void *base, uint32_t bytes) {
+  // raw buffer, stride 0, num_records = bytes (word 3 of the gfx9 buffer descriptor)
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int BM, int BN, int WM, int WN, int ACT>
+__device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, int tiles_n) {
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  constexpr int GROUPS = (BM + BN) / 8;
+  constexpr int P = GROUPS / NW;
+  static_assert(P * NW == GROUPS, "row groups must split evenly over the wavefronts");
+  static_assert((BN & (BN - 1)) == 0, "the epilogue's chunk rotation needs a power-of-two BN");
+  static_assert(BM * BN * 2 <= 2 * (BM + BN) * 128, "the output tile must fit the slab ring");
+  constexpr int STAGE = (BM + BN) * 128;
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+  const int tile = xcd_tile(blockIdx.x, tiles_m * tiles_n);
+  const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int lg = lane >> 5;
+
+  const int rows_a = min(BM, g.M - m0), rows_w = min(BN, g.N - n0);
+  const rsrc_t ra = panel_rsrc((const half_t *)g.a + (int64_t)m0 * g.lda, (uint32_t)(rows_a * g.lda * 2));
+  const rsrc_t rw = panel_rsrc((const half_t *)g.w + (int64_t)n0 * g.ldw, (uint32_t)(rows_w * g.ldw * 2));
+  // load p of this wavefront fills 8-row group wave * P + p: lane l writes row l / 8, position l % 8
+  uint32_t voff[P];
+#pragma unroll
+  for (int p = 0; p < P; p++) {
+    const int r = (wave * P + p) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ swz(r);
+    voff[p] = r < BM ? (uint32_t)((r * g.lda + c * 8) * 2) : (uint32_t)(((r - BM) * g.ldw + c * 8) * 2);
+  }
+  auto issue = [&](int stage, int k0) {
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+      const int grp = wave * P + p;
+      char *dst = smem + stage * STAGE + grp * 1024;
+      if (grp * 8 < BM)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)dst, 16, voff[p], k0 * 2, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void *)dst, 16, voff[p], k0 * 2, 0, 0);
+    }
+  };
+
+  const int arow = wm * TM + (lane & 31);
+  const int brow = BM + wn * TN + (lane & 31);
+  int aaddr[4], baddr[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; kk++) {
+    aaddr[kk] = arow * 128 + (((kk * 2 + lg) ^ swz(arow)) << 4);
+    baddr[kk] = brow * 128 + (((kk * 2 + lg) ^ swz(brow)) << 4);
+  }
+
+  float16v acc[FM][FN];
+  const int nk = g.K / 64;
+  issue(0, 0);
+
+  auto slab = [&](const char *base, auto first_t) {
+    constexpr bool first = decltype(first_t)::value;
+    half8v af[2][FM], bf[2][FN];
+    auto rd = [&](int kk, int s) {
+#pragma unroll
+      for (int i = 0; i < FM; i++) af[s][i] = *reinterpret_cast<const half8v *>(base + aaddr[kk] + i * 4096);
+#pragma unroll
+      for (int j = 0; j < FN; j++) bf[s][j] = *reinterpret_cast<const half8v *>(base + baddr[kk] + j * 4096);
+    };
+    rd(0, 0);
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      if (kk + 1 < 4) rd(kk + 1, (kk + 1) & 1);
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          if (first && kk == 0) {
+            const float16v zero = {};
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[0][j], af[0][i], zero, 0, 0, 0);
+          } else {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[kk & 1][j], af[kk & 1][i], acc[i][j], 0, 0, 0);
+          }
+        }
+    }
+  };
+
+  // slab it in stage it % 2: wait for this wavefront's loads of it, then a barrier (every part
+  // landed, and the stage the next issue overwrites is no longer read)
+  for (int it = 0; it < nk; it += 2) {
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    if (it + 1 < nk) issue(1, (it + 1) * 64);
+    if (it == 0) slab(smem, std::true_type{});
+    else slab(smem, std::false_type{});
+    if (it + 1 >= nk) break;
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    if (it + 2 < nk) issue(0, (it + 2) * 64);
+    slab(smem + STAGE, std::false_type{});
+  }
+
+  // epilogue: acc[i][j][4 q + e] is C[m0 + arow + 32 i][n0 + wn TN + 32 j + 8 q + 4 lg + e]; the
+  // tile goes row-major into LDS (16-byte chunks of a row rotated by the row) and leaves as
+  // whole 16-byte chunks
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  constexpr int RB = BN * 2, CPR = BN / 8;
+  const half_t *bias = (const half_t *)g.bias;
+#pragma unroll
+  for (int j = 0; j < FN; j++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int nl = wn * TN + j * 32 + 8 * q;
+      const int n = n0 + nl + 4 * lg;
+      float b[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bias && n < g.N) {
+        const half4v bv = *reinterpret_cast<const half4v *>(bias + n);
+        b[0] = (float)bv[0]; b[1] = (float)bv[1]; b[2] = (float)bv[2]; b[3] = (float)bv[3];
+      }
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+        const int ml = arow + i * 32;
+        half4v o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[e] = (half_t)act_fn<ACT>(acc[i][j][4 * q + e] + b[e]);
+        const int chunk = ((nl >> 3) + ml) & (CPR - 1);
+        *reinterpret_cast<half4v *>(smem + ml * RB + chunk * 16 + lg * 8) = o;
+      }
+    }
+  __syncthreads();
+  half_t *C = (half_t *)g.c;
+#pragma unroll
+  for (int q = threadIdx.x; q < BM * CPR; q += 64 * NW) {
+    const int row = q / CPR, cc = q % CPR;
+    const int grow = m0 + row, gcol = n0 + cc * 8;
+    if (grow < g.M && gcol < g.N) {
+      const int chunk = (cc + row) & (CPR - 1);
+      *reinterpret_cast<uint4 *>(C + (int64_t)grow * g.ldc + gcol) =
+          *reinterpret_cast<const uint4 *>(smem + row * RB + chunk * 16);
+    }
+  }
+}
+
+// (the body is a device function: the buffer-resource type exists only in device compilation)
+template <int BM, int BN, int WM, int WN, int ACT>
+__global__ void __launch_bounds__(64 * WM * WN)
+__attribute__((amdgpu_waves_per_eu(waves_per_simd<BM, BN, WM, WN, 2>(), waves_per_simd<BM, BN, WM, WN, 2>())))
+gemm_lean_kernel(GemmArgs g, int tiles_m, int tiles_n) {
+  gemm_lean_body<BM, BN, WM, WN, ACT>(g, tiles_m, tiles_n);
+}
+
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 template <typename K>
@@ -578,6 +750,26 @@ void launch_persist(const GemmArgs &g, hipStream_t s, int blocks_per_cu) {
                      g, tm, tn);
 }
 
+
+template <int BM, int BN, int WM, int WN, int ACT>
+void launch_lean(const GemmArgs &g, hipStream_t s) {
+  const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+  constexpr int smem = 2 * (BM + BN) * 128;
+  static bool configured = false;
+  if (!configured) {
+    set_smem(gemm_lean_kernel<BM, BN, WM, WN, ACT>, smem);
+    configured = true;
+  }
+  hipLaunchKernelGGL((gemm_lean_kernel<BM, BN, WM, WN, ACT>), dim3(tm * tn), dim3(64 * WM * WN), smem, s, g, tm, tn);
+}
+
+// shapes the lean kernel runs: f16, one matrix, whole 64-wide k slabs, 16-byte output chunks, and
+// panel byte offsets within 32 bits
+bool lean_ok(const GemmArgs &g) {
+  return !g.c_f32 && g.batch == 1 && g.K % 64 == 0 && g.N % 8 == 0 && g.ldc % 8 == 0 &&
+         (int64_t)256 * g.lda * 2 < ((int64_t)1 << 31) && (int64_t)256 * g.ldw * 2 < ((int64_t)1 << 31);
+}
+
 template <typename T, int ACT>
 void launch_reg(const GemmArgs &g, hipStream_t s) {
   const int tm = (g.M + 127) / 128, tn = (g.N + 127) / 128;
@@ -593,15 +785,19 @@ void launch_reg(const GemmArgs &g, hipStream_t s) {
 
 constexpr int CUS = 256;
 
-// DMA tile configurations: 0 = 256x256 (8 wavefronts of 128x64, 2 stages), 1 = 256x128 (4 of
-// 128x64, 3 stages), 2 = 128x128 (4 of 64x64, 4 stages), 3 = 128x128 (4 of 64x64, 2 stages, two
-// blocks per CU), 4 = 256x256 (4 of 128x128, 2 stages). KH_GEMM_TILE forces one (tuning runs).
-int pick_tile(const GemmArgs &g) {
+// Tile configurations. Lean f16 kernel: 8 = 192x128 (4 wavefronts of 96x64, two blocks per CU),
+// 9 = 192x256 (8 wavefronts of 96x64), 10 = 128x128 (4 of 64x64). DMA kernel: 0 = 256x256 (8 of
+// 128x64, 2 stages), 1 = 256x128 (4 of 128x64, 3 stages), 2 = 128x128 (4 of 64x64, 4 stages),
+// 3 = 128x128 (4 of 64x64, 2 stages, two blocks per CU), 4 = 256x256 (4 of 128x128); persistent
+// 5/6/7. KH_GEMM_TILE forces one (tuning runs).
+int pick_tile(const GemmArgs &g, bool lean) {
   const char *e = getenv("KH_GEMM_TILE");
   const int forced = e ? atoi(e) : -1;
-  if (forced >= 0 && forced <= 7) return forced;
-  // measured on MI355X (f16, random data): 128x128 with two blocks per CU leads on the ragged-batch
-  // shapes (M ~ 13k); the persistent 256x256 kernel leads once M is large and N wide
+  if (forced >= 0 && forced <= 10 && (forced < 8 || lean)) return forced;
+  // measured on MI355X (f16, random data, encoder shapes M = 13k .. 1.2M): 192x128 leads in
+  // general; 192x256 where N is a multiple of 256 and either narrow (N <= 768: one round of tiles
+  // at M ~ 13k) or fed by a short K (<= 384, where the epilogue weighs most)
+  if (lean) return g.N % 256 == 0 && (g.N <= 768 || g.K <= 384) ? 9 : 8;
   if (g.batch == 1 && g.M >= 65536 && g.N >= 1024) return 6;
   return 3;
 }
@@ -612,8 +808,17 @@ void launch_act(const GemmArgs &g, hipStream_t s) {
     launch_reg<T, ACT>(g, s);
     return;
   }
-  int cfg = pick_tile(g);
-  if (cfg >= 5 && g.batch > 1) cfg = 3;  // the persistent kernels walk one matrix
+  const bool lean = sizeof(T) == 2 && lean_ok(g);
+  int cfg = pick_tile(g, lean);
+  if (cfg >= 5 && cfg <= 7 && g.batch > 1) cfg = 3;  // the persistent kernels walk one matrix
+  if constexpr (sizeof(T) == 2) {
+    switch (cfg) {
+      case 8: launch_lean<192, 128, 2, 2, ACT>(g, s); return;
+      case 9: launch_lean<192, 256, 2, 4, ACT>(g, s); return;
+      case 10: launch_lean<128, 128, 2, 2, ACT>(g, s); return;
+      default: break;
+    }
+  }
   switch (cfg) {
     case 5: launch_persist<T, 128, 128, 2, 2, 2, ACT>(g, s, 2); break;
     case 6: launch_persist<T, 256, 256, 2, 4, 2, ACT>(g, s, 1); break;

@@ -77,7 +77,8 @@ def close(got, want, tol, what):
 
 @pytest.mark.parametrize("f16", [False, True])
 @pytest.mark.parametrize("N,K,lens", [(384, 768, [5, 130]), (2304, 768, [257]), (37, 64, [7, 3]),
-                                      (3, 768, [1, 4]), (1536, 384, [64, 64, 1]), (200, 136, [129])])
+                                      (3, 768, [1, 4]), (1536, 384, [64, 64, 1]), (200, 136, [129]),
+                                      (768, 3072, [300, 77]), (3072, 768, [193]), (768, 768, [1])])
 def test_matmul_against_f64(f16, N, K, lens):
     L = max(lens)
     B = len(lens)
@@ -95,6 +96,27 @@ def test_matmul_against_f64(f16, N, K, lens):
         want = ACTS[act](A.astype(np.float64) @ W.astype(np.float64).T + bias.astype(np.float64))
         close(out[valid], want[valid], 5e-3 if f16 else 2e-5, f"act {act} f16 {f16}")
         assert np.all(out[~valid] == 0), "padding rows must read back as zero"
+
+
+@pytest.mark.parametrize("tile", list(range(11)))
+def test_matmul_every_tile_configuration(tile, monkeypatch):
+    """Each GEMM tile configuration (forced through KH_GEMM_TILE) on a ragged f16 batch whose rows
+    end inside a tile, against f64."""
+    monkeypatch.setenv("KH_GEMM_TILE", str(tile))
+    N, K, lens = 768, 1536, [211, 5, 64]
+    L, B = max(lens), len(lens)
+    W = (RNG.standard_normal((N, K)) * 0.05).astype(np.float16)
+    bias = (RNG.standard_normal(N) * 0.1).astype(np.float16)
+    A = RNG.standard_normal((L * B, K)).astype(np.float16)
+    mask = prefix_mask(L, lens)
+    for act in (0, 2):
+        op = {"name": "mm", "kernel": "mmtile", "constants": {"M": L * B, "N": N, "K": K, "ACT": act},
+              "bind": ["emb", "w:w", "w:b", "c"], "dispatch": [math.ceil(N / 64), "rows32"]}
+        plan = mini_plan(True, L, B, K, [op], {"c": L * B * N}, "c", N)
+        out = run_plan(plan, {"w": W, "b": bias}, A, mask, L * B).reshape(L * B, N)
+        valid = mask > 0.5
+        want = ACTS[act](A.astype(np.float64) @ W.astype(np.float64).T + bias.astype(np.float64))
+        close(out[valid], want[valid], 5e-3, f"tile {tile} act {act}")
 
 
 @pytest.mark.parametrize("f16", [False, True])
