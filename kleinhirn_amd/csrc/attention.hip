@@ -232,8 +232,8 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
 template <typename T, bool REL>
 void launch_t(const AttnArgs &a, const Packing &p, hipStream_t s) {
   dim3 grid((unsigned)a.ntiles, (unsigned)a.H);
-  if (a.D == 64) hipLaunchKernelGGL((attn_kernel<T, 64, REL>), grid, dim3(128), 0, s, a, p);
-  else hipLaunchKernelGGL((attn_kernel<T, 32, REL>), grid, dim3(128), 0, s, a, p);
+  if (a.D == 64) launch((attn_kernel<T, 64, REL>), grid, dim3(128), 0, s, a, p);
+  else launch((attn_kernel<T, 32, REL>), grid, dim3(128), 0, s, a, p);
 }
 
 }  // namespace

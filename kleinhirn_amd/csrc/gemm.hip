@@ -732,7 +732,7 @@ void launch_dma(const GemmArgs &g, hipStream_t s) {
     configured = true;
   }
   dim3 grid((unsigned)(tm * tn), 1, (unsigned)g.batch);
-  hipLaunchKernelGGL((gemm_dma_kernel<T, BM, BN, WM, WN, STAGES, ACT>), grid, dim3(64 * WM * WN), smem, s, g, tm,
+  launch((gemm_dma_kernel<T, BM, BN, WM, WN, STAGES, ACT>), grid, dim3(64 * WM * WN), smem, s, g, tm,
                      tn);
 }
 
@@ -746,7 +746,7 @@ void launch_persist(const GemmArgs &g, hipStream_t s, int blocks_per_cu) {
     configured = true;
   }
   const int grid = std::min(tm * tn, 256 * blocks_per_cu);
-  hipLaunchKernelGGL((gemm_persist_kernel<T, BM, BN, WM, WN, STAGES, ACT>), dim3(grid), dim3(64 * WM * WN), smem, s,
+  launch((gemm_persist_kernel<T, BM, BN, WM, WN, STAGES, ACT>), dim3(grid), dim3(64 * WM * WN), smem, s,
                      g, tm, tn);
 }
 
@@ -760,7 +760,7 @@ void launch_lean(const GemmArgs &g, hipStream_t s) {
     set_smem(gemm_lean_kernel<BM, BN, WM, WN, ACT>, smem);
     configured = true;
   }
-  hipLaunchKernelGGL((gemm_lean_kernel<BM, BN, WM, WN, ACT>), dim3(tm * tn), dim3(64 * WM * WN), smem, s, g, tm, tn);
+  launch((gemm_lean_kernel<BM, BN, WM, WN, ACT>), dim3(tm * tn), dim3(64 * WM * WN), smem, s, g, tm, tn);
 }
 
 // shapes the lean kernel runs: f16, one matrix, whole 64-wide k slabs, 16-byte output chunks, and
@@ -780,7 +780,7 @@ void launch_reg(const GemmArgs &g, hipStream_t s) {
     configured = true;
   }
   dim3 grid((unsigned)(tm * tn), 1, (unsigned)g.batch);
-  hipLaunchKernelGGL((gemm_reg_kernel<T, ACT>), grid, dim3(256), smem, s, g, tm, tn);
+  launch((gemm_reg_kernel<T, ACT>), grid, dim3(256), smem, s, g, tm, tn);
 }
 
 constexpr int CUS = 256;
@@ -858,8 +858,8 @@ void gemm(bool f16, const GemmArgs &g, hipStream_t s) {
   } else {
     const int64_t waves = (int64_t)g.M * ((g.N + 3) / 4);
     dim3 grid((unsigned)((waves + 3) / 4), 1, (unsigned)g.batch);
-    if (f16) hipLaunchKernelGGL((gemm_rowdot_kernel<half_t>), grid, dim3(256), 0, s, g);
-    else hipLaunchKernelGGL((gemm_rowdot_kernel<float>), grid, dim3(256), 0, s, g);
+    if (f16) launch((gemm_rowdot_kernel<half_t>), grid, dim3(256), 0, s, g);
+    else launch((gemm_rowdot_kernel<float>), grid, dim3(256), 0, s, g);
   }
 }
 

@@ -3,9 +3,28 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <cstdint>
+#include <utility>
 
 namespace kh {
+
+// Events the next kernel launch of this thread records around itself (the per-launch profile sets
+// them for one step at a time; null otherwise). hipExtLaunchKernelGGL timestamps the dispatch
+// itself, so the measured time is the kernel's, without the gaps of separate event packets.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local LaunchEvents g_launch_events;
+
+template <typename... KArgs, typename... Args>
+inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, unsigned smem, hipStream_t s, Args &&...args) {
+  if (g_launch_events.start)
+    hipExtLaunchKernelGGL(kernel, grid, block, smem, s, g_launch_events.start, g_launch_events.stop, 0,
+                          std::forward<Args>(args)...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, smem, s, std::forward<Args>(args)...);
+}
 
 // Activation codes of the plan's matmul ACT constant (src/plan/build.ts:91).
 enum Act : int { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2, ACT_TANH = 3, ACT_SILU = 4 };

@@ -144,7 +144,7 @@ void layernorm_t(const void *a, const void *b, const void *gamma, const void *be
     constexpr int VEC = decltype(vec)::value;
     dispatch_per<T, VEC>(N, [&](auto per) {
       constexpr int PER = decltype(per)::value;
-      hipLaunchKernelGGL((layernorm_kernel<T, VEC, PER>), grid, dim3(256), 0, s, (const T *)a, (const T *)b,
+      launch((layernorm_kernel<T, VEC, PER>), grid, dim3(256), 0, s, (const T *)a, (const T *)b,
                          (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps);
     });
   };
@@ -160,7 +160,7 @@ void embln_t(const EmbLnArgs &a, const Packing &p, hipStream_t s) {
     constexpr int VEC = decltype(vec)::value;
     dispatch_per<T, VEC>(a.N, [&](auto per) {
       constexpr int PER = decltype(per)::value;
-      hipLaunchKernelGGL((embln_kernel<T, VEC, PER>), grid, dim3(256), 0, s, a, p);
+      launch((embln_kernel<T, VEC, PER>), grid, dim3(256), 0, s, a, p);
     });
   };
   if (a.N % 4 == 0) go(std::integral_constant<int, 4>());
@@ -309,16 +309,16 @@ void add(bool f16, void *dst, const void *src, int64_t rows, int N, int mode, co
   int64_t total = rows * N;
   if (total <= 0) return;
   if (mode == 0 && f16 && total % 8 == 0) {
-    hipLaunchKernelGGL((add_vec_kernel<half8v, half_t, 8>), dim3(grid_for(total / 8)), dim3(256), 0, s,
+    launch((add_vec_kernel<half8v, half_t, 8>), dim3(grid_for(total / 8)), dim3(256), 0, s,
                        (half_t *)dst, (const half_t *)src, total / 8);
   } else if (mode == 0 && !f16 && total % 4 == 0) {
-    hipLaunchKernelGGL((add_vec_kernel<float4v, float, 4>), dim3(grid_for(total / 4)), dim3(256), 0, s,
+    launch((add_vec_kernel<float4v, float, 4>), dim3(grid_for(total / 4)), dim3(256), 0, s,
                        (float *)dst, (const float *)src, total / 4);
   } else if (f16) {
-    hipLaunchKernelGGL((add_kernel<half_t>), dim3(grid_for(total)), dim3(256), 0, s, (half_t *)dst,
+    launch((add_kernel<half_t>), dim3(grid_for(total)), dim3(256), 0, s, (half_t *)dst,
                        (const half_t *)src, total, N, mode, p.row_seq);
   } else {
-    hipLaunchKernelGGL((add_kernel<float>), dim3(grid_for(total)), dim3(256), 0, s, (float *)dst,
+    launch((add_kernel<float>), dim3(grid_for(total)), dim3(256), 0, s, (float *)dst,
                        (const float *)src, total, N, mode, p.row_seq);
   }
 }
@@ -327,17 +327,17 @@ void geglu(bool f16, const void *mid, void *gate, int64_t rows, int I, hipStream
   if (rows <= 0) return;
   if (f16) {
     if (I % 8 == 0)
-      hipLaunchKernelGGL((geglu_kernel<half_t, 8>), dim3(grid_for(rows * I / 8)), dim3(256), 0, s,
+      launch((geglu_kernel<half_t, 8>), dim3(grid_for(rows * I / 8)), dim3(256), 0, s,
                          (const half_t *)mid, (half_t *)gate, rows, I);
     else
-      hipLaunchKernelGGL((geglu_kernel<half_t, 1>), dim3(grid_for(rows * I)), dim3(256), 0, s,
+      launch((geglu_kernel<half_t, 1>), dim3(grid_for(rows * I)), dim3(256), 0, s,
                          (const half_t *)mid, (half_t *)gate, rows, I);
   } else {
     if (I % 4 == 0)
-      hipLaunchKernelGGL((geglu_kernel<float, 4>), dim3(grid_for(rows * I / 4)), dim3(256), 0, s,
+      launch((geglu_kernel<float, 4>), dim3(grid_for(rows * I / 4)), dim3(256), 0, s,
                          (const float *)mid, (float *)gate, rows, I);
     else
-      hipLaunchKernelGGL((geglu_kernel<float, 1>), dim3(grid_for(rows * I)), dim3(256), 0, s,
+      launch((geglu_kernel<float, 1>), dim3(grid_for(rows * I)), dim3(256), 0, s,
                          (const float *)mid, (float *)gate, rows, I);
   }
 }
@@ -348,10 +348,10 @@ void rope(bool f16, void *qkv, const float *cossin, int64_t rows, int H, int D, 
   int64_t total = rows * 2 * H * (D / 2);
   if (total <= 0) return;
   if (f16)
-    hipLaunchKernelGGL((rope_kernel<half_t>), dim3(grid_for(total)), dim3(256), 0, s, (half_t *)qkv, cossin,
+    launch((rope_kernel<half_t>), dim3(grid_for(total)), dim3(256), 0, s, (half_t *)qkv, cossin,
                        rows, H, D, p.row_pos);
   else
-    hipLaunchKernelGGL((rope_kernel<float>), dim3(grid_for(total)), dim3(256), 0, s, (float *)qkv, cossin, rows,
+    launch((rope_kernel<float>), dim3(grid_for(total)), dim3(256), 0, s, (float *)qkv, cossin, rows,
                        H, D, p.row_pos);
 }
 
@@ -359,10 +359,10 @@ void pool(bool f16, const void *x, void *out, int N, int mode, const Packing &p,
   if (p.B <= 0) return;
   dim3 grid((unsigned)((N + 63) / 64), (unsigned)p.B);
   if (f16)
-    hipLaunchKernelGGL((pool_kernel<half_t>), grid, dim3(64), 0, s, (const half_t *)x, (half_t *)out, N, mode,
+    launch((pool_kernel<half_t>), grid, dim3(64), 0, s, (const half_t *)x, (half_t *)out, N, mode,
                        p.cu);
   else
-    hipLaunchKernelGGL((pool_kernel<float>), grid, dim3(64), 0, s, (const float *)x, (float *)out, N, mode, p.cu);
+    launch((pool_kernel<float>), grid, dim3(64), 0, s, (const float *)x, (float *)out, N, mode, p.cu);
 }
 
 void gather_rows(bool f16, const void *x, const uint32_t *markers, void *states, int K, int D, const Packing &p,
@@ -370,19 +370,19 @@ void gather_rows(bool f16, const void *x, const uint32_t *markers, void *states,
   int64_t total = (int64_t)p.B * K * D;
   if (total <= 0) return;
   if (f16)
-    hipLaunchKernelGGL((gather_kernel<half_t>), dim3(grid_for(total)), dim3(256), 0, s, (const half_t *)x, markers,
+    launch((gather_kernel<half_t>), dim3(grid_for(total)), dim3(256), 0, s, (const half_t *)x, markers,
                        (half_t *)states, K, D, p.B, p.cu);
   else
-    hipLaunchKernelGGL((gather_kernel<float>), dim3(grid_for(total)), dim3(256), 0, s, (const float *)x, markers,
+    launch((gather_kernel<float>), dim3(grid_for(total)), dim3(256), 0, s, (const float *)x, markers,
                        (float *)states, K, D, p.B, p.cu);
 }
 
 void to_f32(bool f16, const void *src, float *dst, int64_t n, hipStream_t s) {
   if (n <= 0) return;
   if (f16)
-    hipLaunchKernelGGL((to_f32_kernel<half_t>), dim3(grid_for(n)), dim3(256), 0, s, (const half_t *)src, dst, n);
+    launch((to_f32_kernel<half_t>), dim3(grid_for(n)), dim3(256), 0, s, (const half_t *)src, dst, n);
   else
-    hipLaunchKernelGGL((to_f32_kernel<float>), dim3(grid_for(n)), dim3(256), 0, s, (const float *)src, dst, n);
+    launch((to_f32_kernel<float>), dim3(grid_for(n)), dim3(256), 0, s, (const float *)src, dst, n);
 }
 
 }  // namespace kh

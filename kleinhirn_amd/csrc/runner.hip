@@ -37,6 +37,8 @@ struct Error : std::runtime_error {
 
 static thread_local std::string g_last_error;
 
+thread_local LaunchEvents g_launch_events;
+
 #define KH_CHECK(call)                                                                            \
   do {                                                                                            \
     hipError_t e_ = (call);                                                                       \
@@ -1220,10 +1222,11 @@ int kh_profile(kh_plan *plan, int32_t rows, kh_launch_stat *out, int32_t cap, in
         r.bytes = by;
         KH_CHECK(hipEventCreate(&r.a));
         KH_CHECK(hipEventCreate(&r.b));
-        KH_CHECK(hipEventRecord(r.a, plan->stream));
         recs.push_back(r);
+        g_launch_events.start = r.a;  // the step's kernel records them around its own dispatch
+        g_launch_events.stop = r.b;
       } else {
-        KH_CHECK(hipEventRecord(recs.back().b, plan->stream));
+        g_launch_events = LaunchEvents();
       }
     };
     KH_CHECK(hipEventRecord(plan->ev0, plan->stream));
@@ -1232,6 +1235,7 @@ int kh_profile(kh_plan *plan, int32_t rows, kh_launch_stat *out, int32_t cap, in
     KH_CHECK(hipStreamSynchronize(plan->stream));
     plan->ran = true;
   } catch (const Error &e) {
+    g_launch_events = LaunchEvents();
     for (auto &r : recs) {
       (void)hipEventDestroy(r.a);
       (void)hipEventDestroy(r.b);
@@ -1239,6 +1243,7 @@ int kh_profile(kh_plan *plan, int32_t rows, kh_launch_stat *out, int32_t cap, in
     latch(plan->ctx, e);
     throw;
   }
+  g_launch_events = LaunchEvents();
   *count = (int32_t)recs.size();
   for (size_t i = 0; i < recs.size(); i++) {
     float ms = 0;

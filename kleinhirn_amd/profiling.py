@@ -20,6 +20,7 @@ import sys
 
 # mangled kernel name fragment -> kh_profile family
 FAMILIES = [
+    ("gemm_lean_kernel", "gemm_mfma"),
     ("gemm_dma_kernel", "gemm_mfma"),
     ("gemm_persist_kernel", "gemm_mfma"),
     ("gemm_reg_kernel", "gemm_mfma"),
