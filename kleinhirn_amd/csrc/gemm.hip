@@ -531,11 +531,29 @@ __global__ void __launch_bounds__(256) gemm_rowdot_kernel(GemmArgs g) {
   const T *a = (const T *)g.a + (int64_t)z * g.a_bs + m * g.lda;
   const T *w = (const T *)g.w + (int64_t)z * g.w_bs;
   float s[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int k = lane; k < g.K; k += 64) {
-    const float x = (float)a[k];
+  constexpr int V = 16 / sizeof(T);  // elements per 16-byte load
+  const bool vec = g.K % V == 0 && g.lda % V == 0 && g.ldw % V == 0 && ((uintptr_t)a & 15) == 0 &&
+                   ((uintptr_t)w & 15) == 0;
+  if (vec) {
+    // 16-byte loads: a K = 768 f16 row is one and a half passes of the wavefront
+    typedef T vec_t __attribute__((ext_vector_type(V)));
+    for (int k = lane * V; k < g.K; k += 64 * V) {
+      const vec_t x = *reinterpret_cast<const vec_t *>(a + k);
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-      if (n0 + c < g.N) s[c] += x * (float)w[(int64_t)(n0 + c) * g.ldw + k];
+      for (int c = 0; c < 4; c++) {
+        if (n0 + c >= g.N) continue;
+        const vec_t y = *reinterpret_cast<const vec_t *>(w + (int64_t)(n0 + c) * g.ldw + k);
+#pragma unroll
+        for (int e = 0; e < V; e++) s[c] += (float)x[e] * (float)y[e];
+      }
+    }
+  } else {
+    for (int k = lane; k < g.K; k += 64) {
+      const float x = (float)a[k];
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        if (n0 + c < g.N) s[c] += x * (float)w[(int64_t)(n0 + c) * g.ldw + k];
+    }
   }
 #pragma unroll
   for (int c = 0; c < 4; c++) s[c] = wave_sum(s[c]);
@@ -786,18 +804,19 @@ void launch_reg(const GemmArgs &g, hipStream_t s) {
 constexpr int CUS = 256;
 
 // Tile configurations. Lean f16 kernel: 8 = 192x128 (4 wavefronts of 96x64, two blocks per CU),
-// 9 = 192x256 (8 wavefronts of 96x64), 10 = 128x128 (4 of 64x64). DMA kernel: 0 = 256x256 (8 of
+// 9 = 192x256 (8 wavefronts of 96x64), 10 = 128x128 (4 of 64x64), 11 = 64x64 (1). DMA kernel: 0 = 256x256 (8 of
 // 128x64, 2 stages), 1 = 256x128 (4 of 128x64, 3 stages), 2 = 128x128 (4 of 64x64, 4 stages),
 // 3 = 128x128 (4 of 64x64, 2 stages, two blocks per CU), 4 = 256x256 (4 of 128x128); persistent
 // 5/6/7. KH_GEMM_TILE forces one (tuning runs).
 int pick_tile(const GemmArgs &g, bool lean) {
   const char *e = getenv("KH_GEMM_TILE");
   const int forced = e ? atoi(e) : -1;
-  if (forced >= 0 && forced <= 10 && (forced < 8 || lean)) return forced;
+  if (forced >= 0 && forced <= 11 && (forced < 8 || lean)) return forced;
   // measured on MI355X (f16, random data, encoder shapes M = 13k .. 1.2M): 192x128 leads in
   // general; 192x256 where N is a multiple of 256 and either narrow (N <= 768: one round of tiles
   // at M ~ 13k) or fed by a short K (<= 384, where the epilogue weighs most)
-  if (lean) return g.N % 256 == 0 && (g.N <= 768 || g.K <= 384) ? 9 : 8;
+  // (a few hundred rows, e.g. a pooled head: 64 x 64 tiles, enough of them to spread over CUs)
+  if (lean) return g.M <= 1024 ? 11 : g.N % 256 == 0 && (g.N <= 768 || g.K <= 384) ? 9 : 8;
   if (g.batch == 1 && g.M >= 65536 && g.N >= 1024) return 6;
   return 3;
 }
@@ -816,6 +835,7 @@ void launch_act(const GemmArgs &g, hipStream_t s) {
       case 8: launch_lean<192, 128, 2, 2, ACT>(g, s); return;
       case 9: launch_lean<192, 256, 2, 4, ACT>(g, s); return;
       case 10: launch_lean<128, 128, 2, 2, ACT>(g, s); return;
+      case 11: launch_lean<64, 64, 1, 1, ACT>(g, s); return;
       default: break;
     }
   }

@@ -148,7 +148,9 @@ void layernorm_t(const void *a, const void *b, const void *gamma, const void *be
                          (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps);
     });
   };
-  if (N % 4 == 0) go(std::integral_constant<int, 4>());
+  // 16-byte loads where the width allows
+  if (N % (16 / sizeof(T)) == 0) go(std::integral_constant<int, 16 / sizeof(T)>());
+  else if (N % 4 == 0) go(std::integral_constant<int, 4>());
   else if (N % 2 == 0) go(std::integral_constant<int, 2>());
   else go(std::integral_constant<int, 1>());
 }
@@ -163,7 +165,8 @@ void embln_t(const EmbLnArgs &a, const Packing &p, hipStream_t s) {
       launch((embln_kernel<T, VEC, PER>), grid, dim3(256), 0, s, a, p);
     });
   };
-  if (a.N % 4 == 0) go(std::integral_constant<int, 4>());
+  if (a.N % (16 / sizeof(T)) == 0) go(std::integral_constant<int, 16 / sizeof(T)>());
+  else if (a.N % 4 == 0) go(std::integral_constant<int, 4>());
   else if (a.N % 2 == 0) go(std::integral_constant<int, 2>());
   else go(std::integral_constant<int, 1>());
 }

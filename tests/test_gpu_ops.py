@@ -78,7 +78,8 @@ def close(got, want, tol, what):
 @pytest.mark.parametrize("f16", [False, True])
 @pytest.mark.parametrize("N,K,lens", [(384, 768, [5, 130]), (2304, 768, [257]), (37, 64, [7, 3]),
                                       (3, 768, [1, 4]), (1536, 384, [64, 64, 1]), (200, 136, [129]),
-                                      (768, 3072, [300, 77]), (3072, 768, [193]), (768, 768, [1])])
+                                      (768, 3072, [300, 77]), (3072, 768, [193]), (768, 768, [1]),
+                                      (2, 768, [3, 1]), (3, 40, [2])])
 def test_matmul_against_f64(f16, N, K, lens):
     L = max(lens)
     B = len(lens)
@@ -98,7 +99,7 @@ def test_matmul_against_f64(f16, N, K, lens):
         assert np.all(out[~valid] == 0), "padding rows must read back as zero"
 
 
-@pytest.mark.parametrize("tile", list(range(11)))
+@pytest.mark.parametrize("tile", list(range(12)))
 def test_matmul_every_tile_configuration(tile, monkeypatch):
     """Each GEMM tile configuration (forced through KH_GEMM_TILE) on a ragged f16 batch whose rows
     end inside a tile, against f64."""
