@@ -50,7 +50,10 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
   typedef AttnMfma<T> MF;
   constexpr int PADK = 16 / sizeof(T);   // 16 bytes of row padding
   constexpr int LDK = D + PADK;           // sK row
-  constexpr int LDV = KT + PADK;          // sVt row
+  // sVt row: 4 elements of padding (a 136-byte pitch for f16): the 4-key column writes of 8
+  // threads 8 rows apart then spread over 4 bank groups, and 16 rows read at one key offset stay in
+  // distinct banks
+  constexpr int LDV = KT + 4;
   constexpr int DT = D / 32;              // 32-wide d sub-tiles of the output
   constexpr int QS = D / MF::KSTEP;       // MFMA k-steps over d
   constexpr int CE = 16 / sizeof(T);      // elements per 16-byte chunk
@@ -98,20 +101,32 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
   float m_run = -INFINITY, l_run = 0.f;
 
   for (int kb = klo; kb < khi; kb += KT) {
-    // K tile [key][d] and V tile transposed [d][key]; rows past khi are zero
-    for (int c = t; c < KT * CPR; c += 128) {
-      const int kr = c / CPR, dc = (c % CPR) * CE;
-      const int j = kb + kr;
-      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-      if (j < khi) {
-        const T *row = qkv + (base + j) * rs;
-        kv = *reinterpret_cast<const uint4 *>(row + (H + h) * D + dc);
-        vv = *reinterpret_cast<const uint4 *>(row + (2 * H + h) * D + dc);
-      }
-      *reinterpret_cast<uint4 *>(&sK[kr * LDK + dc]) = kv;
-      const T *ve = reinterpret_cast<const T *>(&vv);
+    // K tile [key][d] and V tile transposed [d][key]; rows past khi are zero. A thread moves one
+    // 16-byte chunk of 4 consecutive keys: K rows as they are, V as 4-key vectors per d.
+    for (int c = t; c < (KT / 4) * CPR; c += 128) {
+      const int kr = (c / CPR) * 4, dc = (c % CPR) * CE;
+      uint4 kv[4], vv[4];
 #pragma unroll
-      for (int e = 0; e < CE; e++) sVt[(dc + e) * LDV + kr] = ve[e];
+      for (int u = 0; u < 4; u++) {
+        const int j = kb + kr + u;
+        kv[u] = make_uint4(0, 0, 0, 0);
+        vv[u] = make_uint4(0, 0, 0, 0);
+        if (j < khi) {
+          const T *row = qkv + (base + j) * rs;
+          kv[u] = *reinterpret_cast<const uint4 *>(row + (H + h) * D + dc);
+          vv[u] = *reinterpret_cast<const uint4 *>(row + (2 * H + h) * D + dc);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) *reinterpret_cast<uint4 *>(&sK[(kr + u) * LDK + dc]) = kv[u];
+      typedef T vec4_t __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int e = 0; e < CE; e++) {
+        vec4_t col;
+#pragma unroll
+        for (int u = 0; u < 4; u++) col[u] = reinterpret_cast<const T *>(&vv[u])[e];
+        *reinterpret_cast<vec4_t *>(&sVt[(dc + e) * LDV + kr]) = col;
+      }
     }
     __syncthreads();
 
@@ -131,7 +146,8 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
       }
     }
 
-    // scale, mask, tile maximum
+    // scale (in base 2: scale * log2 e, so exp2 gives the same weights as exp), mask, maximum
+    const float scale2 = a.scale * 1.4426950408889634f;
     float tmax = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
@@ -150,22 +166,22 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
             v += a.c2p[((base + qi) * H + h) * a.nb + m] + a.p2c[((base + j) * H + h) * a.nb + m];
           }
         }
-        v = ok ? v * a.scale : -INFINITY;
+        v = ok ? v * scale2 : -INFINITY;
         sc[kt][r] = v;
         tmax = fmaxf(tmax, v);
       }
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
     const float m_new = fmaxf(m_run, tmax);
-    // a query with no key in this tile keeps its state (corr 1, p 0)
-    const float corr = m_new == -INFINITY ? 1.f : __expf(m_run - m_new);
+    // a query with no key so far keeps its state (corr 1, weights exp2(-inf) = 0)
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
     float psum = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const float v = sc[kt][r];
-        const float e = v == -INFINITY ? 0.f : __expf(v - m_new);
+        const float e = __builtin_amdgcn_exp2f(sc[kt][r] - m_use);
         sc[kt][r] = e;
         psum += e;
       }
@@ -218,13 +234,17 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
   if (!qvalid) return;
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   T *out = (T *)a.ctx + (base + qi) * (int64_t)H * D + h * D;
+  typedef T vec4_t __attribute__((ext_vector_type(4)));
 #pragma unroll
   for (int dt = 0; dt < DT; dt++) {
 #pragma unroll
     for (int r4 = 0; r4 < 4; r4++) {
+      // registers 4 r4 .. 4 r4 + 3 hold d .. d + 3 of this lane's query: one vector store
       const int d = dt * 32 + 8 * r4 + 4 * g;
+      vec4_t v;
 #pragma unroll
-      for (int e = 0; e < 4; e++) out[d + e] = (T)(o[dt][4 * r4 + e] * inv);
+      for (int e = 0; e < 4; e++) v[e] = (T)(o[dt][4 * r4 + e] * inv);
+      *reinterpret_cast<vec4_t *>(out + d) = v;
     }
   }
 }
