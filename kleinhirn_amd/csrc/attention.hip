@@ -13,8 +13,13 @@
 // and never enter the maximum; packed rows are all valid queries and keys, so every query keeps at
 // least itself and the normaliser is positive.
 //
-// DeBERTa relative attention adds (c2p[i][h][m] + p2c[j][h][m]) with m = bucket(i - j) to q.k
-// before the scale (src/wasm/plan.ts:791-840); c2p and p2c come from the relative-position GEMMs.
+// DeBERTa relative attention adds q_i . pos_key[m] + k_j . pos_query[m] with m = bucket(i - j) to
+// q_i . k_j before the scale (src/wasm/plan.ts:791-840). Buckets are monotone in i - j, so the 32
+// queries of a wavefront and a 32-key sub-tile reach at most 63 consecutive buckets: per sub-tile
+// the wavefront computes both terms for those 64 position rows on MFMA (pos_key rows x its Q,
+// pos_query rows x the sub-tile's K), parks them in its own LDS scratch (row pitch 68 floats, so
+// the diagonal reads of one register across lanes hit distinct banks) and adds each score's two
+// entries from there. The position tables are read from L2; no [T, H, buckets] array exists.
 #include "kernels.h"
 #include "device.h"
 
@@ -23,6 +28,7 @@ namespace kh {
 namespace {
 
 constexpr int QT = ATTN_QTILE;  // queries per block (2 wavefronts x 32)
+constexpr int REL_BUCKETS = 2 * ATTN_REL_LMAX - 1;  // bucket table entries cached in LDS
 constexpr int KT = 64;          // keys per LDS tile
 
 template <typename T>
@@ -60,6 +66,9 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
   constexpr int CPR = D / CE;             // chunks per key row
   __shared__ __attribute__((aligned(16))) T sK[KT * LDK];
   __shared__ __attribute__((aligned(16))) T sVt[D * LDV];
+  constexpr int RP = 68;  // relative scratch pitch (floats)
+  __shared__ __attribute__((aligned(16))) float sRel[REL ? 2 * 2 * 32 * RP : 1];  // [wave][c2p|p2c][32][RP]
+  __shared__ int sBucket[REL ? REL_BUCKETS : 1];
 
   const int2 tile = a.tiles[blockIdx.x];
   const int b = tile.x, q0 = tile.y;
@@ -99,6 +108,10 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
 #pragma unroll
     for (int r = 0; r < 16; r++) o[dt][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
+  if constexpr (REL) {
+    // visible to every wavefront after the first K/V staging barrier
+    for (int i = t; i < 2 * a.lmax - 1; i += 128) sBucket[i] = a.bucket[i];
+  }
 
   for (int kb = klo; kb < khi; kb += KT) {
     // K tile [key][d] and V tile transposed [d][key]; rows past khi are zero. A thread moves one
@@ -151,9 +164,58 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
     float tmax = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
+      [[maybe_unused]] int mlo = 0;
+      [[maybe_unused]] const float *c2pW = nullptr;
+      [[maybe_unused]] const float *p2cW = nullptr;
+      if constexpr (REL) {
+        // buckets reachable from this wavefront's queries and sub-tile kt's keys
+        const int kj0 = kb + kt * 32, qw0 = q0 + w * 32;
+        int dlo = qw0 - (kj0 + 31);
+        dlo = dlo < 1 - a.lmax ? 1 - a.lmax : (dlo > a.lmax - 1 ? a.lmax - 1 : dlo);
+        mlo = sBucket[dlo + a.lmax - 1];
+        float *c2pw = sRel + (w * 2) * 32 * RP;
+        float *p2cw = c2pw + 32 * RP;
+        const int64_t hd = (int64_t)H * D;
+        const int prow = mlo + (lane & 31);
+        const T *krow = &sK[(kt * 32 + (lane & 31)) * LDK + g * MF::KLANE];
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+          const int pr = prow + mt * 32 < a.nb ? prow + mt * 32 : a.nb - 1;
+          const T *pk = (const T *)a.pos_key + pr * hd + h * D + g * MF::KLANE;
+          const T *pq = (const T *)a.pos_query + pr * hd + h * D + g * MF::KLANE;
+          float16v cq = {}, ck = {};
+#pragma unroll
+          for (int s = 0; s < QS; s++) {
+            typename MF::frag fk, fq, kf;
+            if constexpr (sizeof(T) == 2) {
+              fk = *reinterpret_cast<const half8v *>(pk + s * MF::KSTEP);
+              fq = *reinterpret_cast<const half8v *>(pq + s * MF::KSTEP);
+              kf = *reinterpret_cast<const half8v *>(krow + s * MF::KSTEP);
+            } else {
+              fk = pk[s * MF::KSTEP];
+              fq = pq[s * MF::KSTEP];
+              kf = krow[s * MF::KSTEP];
+            }
+            cq = MF::mma(fk, qf[s], cq);  // [m][query]: lane = query
+            ck = MF::mma(fq, kf, ck);     // [m][key]: lane = key
+          }
+          // registers 4 r4 .. 4 r4 + 3 are buckets mlo + 32 mt + 8 r4 + 4 g + {0..3}
+#pragma unroll
+          for (int r4 = 0; r4 < 4; r4++) {
+            const int mm = mt * 32 + 8 * r4 + 4 * g;
+            *reinterpret_cast<float4v *>(&c2pw[(lane & 31) * RP + mm]) =
+                float4v{cq[4 * r4], cq[4 * r4 + 1], cq[4 * r4 + 2], cq[4 * r4 + 3]};
+            *reinterpret_cast<float4v *>(&p2cw[(lane & 31) * RP + mm]) =
+                float4v{ck[4 * r4], ck[4 * r4 + 1], ck[4 * r4 + 2], ck[4 * r4 + 3]};
+          }
+        }
+        c2pW = c2pw + (lane & 31) * RP - mlo;  // this lane's query row, indexed by bucket
+        p2cW = p2cw - mlo;
+      }
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int j = kb + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        const int jl = 8 * (r >> 2) + 4 * g + (r & 3);
+        const int j = kb + kt * 32 + jl;
         bool ok = qvalid && j < khi;
         if (a.window > 0) {
           const int dist = qi > j ? qi - j : j - qi;
@@ -162,8 +224,9 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
         float v = sc[kt][r];
         if constexpr (REL) {
           if (ok) {
-            const int m = a.bucket[qi - j + a.lmax - 1];
-            v += a.c2p[((base + qi) * H + h) * a.nb + m] + a.p2c[((base + j) * H + h) * a.nb + m];
+            const int m = sBucket[qi - j + a.lmax - 1];
+            v = v + c2pW[m];
+            v = v + p2cW[jl * RP + m];
           }
         }
         v = ok ? v * scale2 : -INFINITY;
@@ -260,7 +323,7 @@ void launch_t(const AttnArgs &a, const Packing &p, hipStream_t s) {
 
 void attention(bool f16, const AttnArgs &a, const Packing &p, hipStream_t s) {
   if (a.ntiles <= 0) return;
-  const bool rel = a.c2p != nullptr;
+  const bool rel = a.pos_key != nullptr;
   if (f16) {
     if (rel) launch_t<half_t, true>(a, p, s);
     else launch_t<half_t, false>(a, p, s);

@@ -102,10 +102,11 @@ struct AttnArgs {
   int H = 0, D = 0;
   float scale = 1.f;          // multiplies the score
   int window = 0;             // 0: global, else |i - j| <= window
-  // DeBERTa relative terms: score = (q.k + c2p[i][h][bucket] + p2c[j][h][bucket]) * scale
-  const float *c2p = nullptr;  // [T, H, NB]
-  const float *p2c = nullptr;  // [T, H, NB]
-  const int32_t *bucket = nullptr;  // [2 Lmax - 1] bucket of (i - j) + Lmax - 1
+  // DeBERTa relative terms: score = (q_i.k_j + q_i.pos_key[m] + k_j.pos_query[m]) * scale with
+  // m = bucket[i - j + lmax - 1]; the position tables are [nb, H D] in the storage type
+  const void *pos_key = nullptr;
+  const void *pos_query = nullptr;
+  const int32_t *bucket = nullptr;  // [2 lmax - 1]
   int nb = 0;
   int lmax = 0;
   const int2 *tiles;
@@ -113,6 +114,7 @@ struct AttnArgs {
 };
 void attention(bool f16, const AttnArgs &a, const Packing &p, hipStream_t s);
 constexpr int ATTN_QTILE = 64;
+constexpr int ATTN_REL_LMAX = 512;  // longest plan the relative attention kernel takes
 
 // Convert storage rows to f32 (readback of f16 outputs).
 void to_f32(bool f16, const void *src, float *dst, int64_t n, hipStream_t s);

@@ -192,8 +192,8 @@ struct kh_plan {
   // relative attention
   std::vector<int32_t> bucket_host;
   DevMem d_bucket;
-  DevMem d_c2p, d_p2c;
   int rel_nb = 0;
+  double rel_rows_buckets = 0;  // sum over sequences of rows x buckets reached (c2p + p2c work)
 
   // cos/sin tables (f32)
   std::map<std::string, std::unique_ptr<DevMem>> tables;
@@ -570,44 +570,17 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
       const double hd = (double)s.H * s.D;
       double pairs = pl->attn_pairs_global;
       if (s.window > 0) pairs = pl->attn_pairs_window[s.window];
+      double rel_fl = 0;
       if (s.rel) {
-        // c2p = q . posKey[m], p2c = k . posQuery[m] over every bucket row m (relative-position GEMMs)
-        const int nb = pl->rel_nb;
-        GemmArgs g;
-        g.lda = 3 * s.H * s.D;
-        g.ldw = s.H * s.D;
-        g.ldc = (int64_t)s.H * nb;
-        g.M = (int)pl->T;
-        g.N = nb;
-        g.K = s.D;
-        g.act = 0;
-        g.batch = s.H;
-        g.a_bs = s.D;
-        g.w_bs = s.D;
-        g.c_bs = nb;
-        g.c_f32 = true;
-        g.bias = nullptr;
-        g.a = a.qkv;
-        g.w = bufp(pl, s.in[2]);
-        g.c = pl->d_c2p.p;
-        const double fl = 2.0 * pl->T * nb * s.D * s.H;
-        const double by = (double)es * (pl->T * hd + (double)nb * hd) + 4.0 * pl->T * s.H * nb;
-        begin("gemm_rel_c2p", fl, by);
-        gemm(f16, g, st);
-        end();
-        g.a = (const char *)a.qkv + (size_t)s.H * s.D * es;
-        g.w = bufp(pl, s.in[3]);
-        g.c = pl->d_p2c.p;
-        begin("gemm_rel_p2c", fl, by);
-        gemm(f16, g, st);
-        end();
-        a.c2p = (const float *)pl->d_c2p.p;
-        a.p2c = (const float *)pl->d_p2c.p;
+        // q . pos_key[m] and k . pos_query[m] over the buckets each sequence reaches, inside the kernel
+        a.pos_key = bufp(pl, s.in[2]);
+        a.pos_query = bufp(pl, s.in[3]);
         a.bucket = (const int32_t *)pl->d_bucket.p;
-        a.nb = nb;
+        a.nb = pl->rel_nb;
         a.lmax = pl->L;
+        rel_fl = 4.0 * hd * pl->rel_rows_buckets;
       }
-      begin(s.rel ? "attention_rel" : "attention", 4.0 * hd * pairs, (double)es * 4.0 * pl->T * hd);
+      begin(s.rel ? "attention_rel" : "attention", 4.0 * hd * pairs + rel_fl, (double)es * 4.0 * pl->T * hd);
       attention(f16, a, pk, st);
       end();
       break;
@@ -665,6 +638,13 @@ static void pack(kh_plan *pl, int rows) {
     }
   }
   pl->ntiles = (int)tiles.size();
+  pl->rel_rows_buckets = 0;
+  if (!pl->bucket_host.empty())
+    for (int b = 0; b < B; b++)
+      if (n[b] > 0)
+        // buckets are monotone in i - j: those of distances -(n - 1) .. n - 1 form one range
+        pl->rel_rows_buckets += (double)n[b] * (pl->bucket_host[(L - 1) + (n[b] - 1)] -
+                                                pl->bucket_host[(L - 1) - (n[b] - 1)] + 1);
   if (tiles.empty()) tiles.push_back(make_int2(0, 0));
 
   // metadata: cu | row_pos | row_seq | tiles | tt | ids, one pinned staging block
@@ -745,14 +725,6 @@ static void ensure_rel(kh_plan *pl) {
   for (const Step &s : pl->steps) rel = rel || s.rel;
   if (!rel) return;
   if (!pl->d_bucket.p) fail(KH_EINVAL, "relative attention needs the relidx table (kh_plan_init_buffer)");
-  int H = 0;
-  for (const Step &s : pl->steps)
-    if (s.rel) H = std::max(H, s.H);
-  const size_t need = (size_t)std::max<int64_t>(pl->T, 1) * H * pl->rel_nb * 4;
-  if (pl->d_c2p.bytes < need) {
-    pl->d_c2p.alloc(need);
-    pl->d_p2c.alloc(need);
-  }
 }
 
 static void run_steps(kh_plan *pl, const LaunchHook &hook) {
@@ -995,6 +967,9 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
       }
     }
     if (s.kind == S_ATTN && s.rel) {
+      if (pl->L > ATTN_REL_LMAX)
+        fail(KH_EUNSUPPORTED, "op " + s.name + ": relative attention over more than " + std::to_string(ATTN_REL_LMAX) +
+                                  " rows per sequence");
       const Weight *pk = weight_of(ctx, s.in[2].id);
       if (!pk || pk->shape.size() != 2 || pk->shape[1] != (int64_t)s.H * s.D)
         fail(KH_EINVAL, "op " + s.name + ": position table must be [2 * buckets, H * D]");
@@ -1028,6 +1003,12 @@ int kh_plan_init_buffer(kh_plan *plan, const char *id, const void *data, size_t 
           fail(KH_EUNSUPPORTED, "relidx is not a function of i - j");
     for (int32_t v : plan->bucket_host)
       if (v < 0 || v >= plan->rel_nb) fail(KH_EINVAL, "relidx entry outside the position table");
+    // the attention kernel takes the buckets of a 32 x 32 sub-tile (63 distances) as one range of
+    // at most 63: buckets must rise by 0 or 1 per unit of i - j
+    for (size_t d = 1; d < plan->bucket_host.size(); d++) {
+      const int32_t step = plan->bucket_host[d] - plan->bucket_host[d - 1];
+      if (step < 0 || step > 1) fail(KH_EUNSUPPORTED, "relidx buckets must rise by 0 or 1 per unit of i - j");
+    }
     plan->d_bucket.alloc(plan->bucket_host.size() * 4);
     KH_CHECK(hipMemcpy(plan->d_bucket.p, plan->bucket_host.data(), plan->bucket_host.size() * 4, hipMemcpyHostToDevice));
     return KH_OK;
@@ -1047,7 +1028,7 @@ int kh_plan_info_get(const kh_plan *plan, kh_plan_info *out) {
   uint64_t bytes = 0;
   for (const auto &kv : plan->bufs)
     if (kv.second.mem) bytes += kv.second.mem->bytes;
-  bytes += plan->d_c2p.bytes + plan->d_p2c.bytes;
+
   out->bytes = bytes;
   out->out_rows = plan->out_rows;
   out->out_cols = plan->out_cols;
