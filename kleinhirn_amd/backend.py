@@ -17,7 +17,8 @@ import numpy as np
 from .plan.build import plan_inits, plan_json
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libkh_hip.so")
+# KH_LIB selects another build of the same library (A/B timing of kernel variants)
+LIB_PATH = os.environ.get("KH_LIB") or os.path.join(HERE, "libkh_hip.so")
 
 KH_F32, KH_F16, KH_U32 = 0, 1, 2
 ERRORS = {1: "EINVAL", 2: "EUNSUPPORTED", 3: "EHIP", 4: "ENOMEM", 5: "ELOST"}

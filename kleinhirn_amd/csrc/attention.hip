@@ -51,8 +51,10 @@ struct AttnMfma<float> {
   }
 };
 
+// Four wavefronts per SIMD on the standard path: short sequences are latency-bound.
 template <typename T, int D, bool REL>
-__global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
+__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(REL ? 1 : 4, 8)))
+attn_kernel(AttnArgs a, Packing p) {
   typedef AttnMfma<T> MF;
   constexpr int PADK = 16 / sizeof(T);   // 16 bytes of row padding
   constexpr int LDK = D + PADK;           // sK row
@@ -159,7 +161,10 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
       }
     }
 
-    // scale (in base 2: scale * log2 e, so exp2 gives the same weights as exp), mask, maximum
+    // Mask and maximum on the raw scores; the scale (in base 2: scale * log2 e, so exp2 gives the
+    // same weights as exp) enters once, inside the exponent. Register r of sub-tile kt is key
+    // kb + 32 kt + jl(r) with jl(r) a constant, so the key-range mask is one compare per score
+    // against a per-lane limit; window bounds add two.
     const float scale2 = a.scale * 1.4426950408889634f;
     float tmax = -INFINITY;
 #pragma unroll
@@ -212,30 +217,32 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
         c2pW = c2pw + (lane & 31) * RP - mlo;  // this lane's query row, indexed by bucket
         p2cW = p2cw - mlo;
       }
+      const int k0 = kb + kt * 32;
+      const int lim = (qvalid ? khi : k0) - k0;             // keys jl < lim exist
+      const int wlo = qi - a.window - k0, whi = qi + a.window - k0;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         const int jl = 8 * (r >> 2) + 4 * g + (r & 3);
-        const int j = kb + kt * 32 + jl;
-        bool ok = qvalid && j < khi;
-        if (a.window > 0) {
-          const int dist = qi > j ? qi - j : j - qi;
-          ok = ok && dist <= a.window;
-        }
+        bool ok = jl < lim;
+        if (a.window > 0) ok = ok && jl >= wlo && jl <= whi;
         float v = sc[kt][r];
         if constexpr (REL) {
-          if (ok) {
-            const int m = sBucket[qi - j + a.lmax - 1];
-            v = v + c2pW[m];
-            v = v + p2cW[jl * RP + m];
-          }
+          // gathered unconditionally (no branch per score): indices clamped into the tables, the
+          // masked pairs' values are discarded below
+          int di = qi - (k0 + jl) + a.lmax - 1;
+          di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
+          int mm = sBucket[di] - mlo;
+          mm = mm < 0 ? 0 : (mm > 63 ? 63 : mm);
+          v = v + c2pW[mlo + mm];
+          v = v + p2cW[jl * RP + mlo + mm];
         }
-        v = ok ? v * scale2 : -INFINITY;
+        v = ok ? v : -INFINITY;
         sc[kt][r] = v;
         tmax = fmaxf(tmax, v);
       }
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
+    const float m_new = fmaxf(m_run, tmax * scale2);
     // a query with no key so far keeps its state (corr 1, weights exp2(-inf) = 0)
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
@@ -244,17 +251,20 @@ __global__ void __launch_bounds__(128) attn_kernel(AttnArgs a, Packing p) {
     for (int kt = 0; kt < 2; kt++) {
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const float e = __builtin_amdgcn_exp2f(sc[kt][r] - m_use);
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][r], scale2, -m_use));
         sc[kt][r] = e;
         psum += e;
       }
     }
     l_run = l_run * corr + psum;
     m_run = m_new;
+    // (once the maxima settle, no lane rescales)
+    if (__any(corr != 1.f)) {
 #pragma unroll
-    for (int dt = 0; dt < DT; dt++)
+      for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) o[dt][r] *= corr;
+        for (int r = 0; r < 16; r++) o[dt][r] *= corr;
+    }
 
     // O^T += V^T P^T: k = keys; lane group g holds keys 4 g + {0..3} and 8 + 4 g + {0..3} of each
     // 16-key half, for both operands
