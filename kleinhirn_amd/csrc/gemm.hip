@@ -589,7 +589,7 @@ __device__ __forceinline__ rsrc_t panel_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-template <int BM, int BN, int WM, int WN, int ACT>
+template <int BM, int BN, int WM, int WN, int ACT, int EPI>
 __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, int tiles_n) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
@@ -610,14 +610,20 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
 
   const int rows_a = min(BM, g.M - m0), rows_w = min(BN, g.N - n0);
   const rsrc_t ra = panel_rsrc((const half_t *)g.a + (int64_t)m0 * g.lda, (uint32_t)(rows_a * g.lda * 2));
-  const rsrc_t rw = panel_rsrc((const half_t *)g.w + (int64_t)n0 * g.ldw, (uint32_t)(rows_w * g.ldw * 2));
+  // GeGLU: the tile's columns are BN / 2 rows of each half of W (all of W in one resource)
+  const rsrc_t rw = EPI == EPI_GEGLU
+                        ? panel_rsrc(g.w, (uint32_t)((int64_t)g.N * g.ldw * 2))
+                        : panel_rsrc((const half_t *)g.w + (int64_t)n0 * g.ldw, (uint32_t)(rows_w * g.ldw * 2));
   // load p of this wavefront fills 8-row group wave * P + p: lane l writes row l / 8, position l % 8
   uint32_t voff[P];
 #pragma unroll
   for (int p = 0; p < P; p++) {
     const int r = (wave * P + p) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ swz(r);
-    voff[p] = r < BM ? (uint32_t)((r * g.lda + c * 8) * 2) : (uint32_t)(((r - BM) * g.ldw + c * 8) * 2);
+    int wr = r - BM;
+    if constexpr (EPI == EPI_GEGLU)
+      wr = (n0 >> 1) + (wr < BN / 2 ? wr : g.N / 2 + wr - BN / 2);
+    voff[p] = r < BM ? (uint32_t)((r * g.lda + c * 8) * 2) : (uint32_t)((wr * g.ldw + c * 8) * 2);
   }
   auto issue = [&](int stage, int k0) {
 #pragma unroll
@@ -713,24 +719,68 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
     }
   __syncthreads();
   half_t *C = (half_t *)g.c;
+  auto chunk_at = [&](int row, int cc) {
+    return *reinterpret_cast<const half8v *>(smem + row * RB + ((cc + row) & (CPR - 1)) * 16);
+  };
+  if constexpr (EPI == EPI_GEGLU) {
+    // output columns n0 / 2 .. n0 / 2 + BN / 2 of C [M, N / 2]: gelu(a) * b, a and b as stored
+    constexpr int HC = CPR / 2;
+    const int I = g.N / 2;
 #pragma unroll
-  for (int q = threadIdx.x; q < BM * CPR; q += 64 * NW) {
-    const int row = q / CPR, cc = q % CPR;
-    const int grow = m0 + row, gcol = n0 + cc * 8;
-    if (grow < g.M && gcol < g.N) {
-      const int chunk = (cc + row) & (CPR - 1);
-      *reinterpret_cast<uint4 *>(C + (int64_t)grow * g.ldc + gcol) =
-          *reinterpret_cast<const uint4 *>(smem + row * RB + chunk * 16);
+    for (int q = threadIdx.x; q < BM * HC; q += 64 * NW) {
+      const int row = q / HC, cc = q % HC;
+      const int grow = m0 + row, gcol = (n0 >> 1) + cc * 8;
+      if (grow < g.M && gcol < I) {
+        const half8v x = chunk_at(row, cc), y = chunk_at(row, cc + HC);
+        half8v o;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = (half_t)(gelu_as((float)x[e]) * (float)y[e]);
+        *reinterpret_cast<half8v *>(C + (int64_t)grow * g.ldc + gcol) = o;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = threadIdx.x; q < BM * CPR; q += 64 * NW) {
+      const int row = q / CPR, cc = q % CPR;
+      const int grow = m0 + row, gcol = n0 + cc * 8;
+      if (grow < g.M && gcol < g.N) {
+        half8v x = chunk_at(row, cc);
+        half_t *dst = C + (int64_t)grow * g.ldc + gcol;
+        if constexpr (EPI == EPI_ROPE) {
+          // rotate-half on q and k: d < D / 2 pairs with d + D / 2 of the same head (tiles start
+          // at head boundaries); cos at table[pos][d], sin at table[pos][D + d]
+          if (gcol < g.rope_cols) {
+            const int D = g.rope_d, half = D >> 1;
+            const int d0 = gcol % D;
+            const bool lo = d0 < half;
+            const half8v y = chunk_at(row, lo ? cc + half / 8 : cc - half / 8);
+            const float *t = g.rope_table + (int64_t)g.row_pos[grow] * 2 * D + (lo ? d0 : d0 - half);
+            half8v o;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+              const float c = t[e], sn = t[D + e];
+              o[e] = lo ? (half_t)((float)x[e] * c - (float)y[e] * sn) : (half_t)((float)x[e] * c + (float)y[e] * sn);
+            }
+            x = o;
+          }
+        } else if constexpr (EPI == EPI_RESADD) {
+          // residual += product, in f32, rounded once (the add op on the stored product)
+          const half8v r = *reinterpret_cast<const half8v *>(dst);
+#pragma unroll
+          for (int e = 0; e < 8; e++) x[e] = (half_t)((float)r[e] + (float)x[e]);
+        }
+        *reinterpret_cast<half8v *>(dst) = x;
+      }
     }
   }
 }
 
 // (the body is a device function: the buffer-resource type exists only in device compilation)
-template <int BM, int BN, int WM, int WN, int ACT>
+template <int BM, int BN, int WM, int WN, int ACT, int EPI>
 __global__ void __launch_bounds__(64 * WM * WN)
 __attribute__((amdgpu_waves_per_eu(waves_per_simd<BM, BN, WM, WN, 2>(), waves_per_simd<BM, BN, WM, WN, 2>())))
 gemm_lean_kernel(GemmArgs g, int tiles_m, int tiles_n) {
-  gemm_lean_body<BM, BN, WM, WN, ACT>(g, tiles_m, tiles_n);
+  gemm_lean_body<BM, BN, WM, WN, ACT, EPI>(g, tiles_m, tiles_n);
 }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -769,16 +819,26 @@ void launch_persist(const GemmArgs &g, hipStream_t s, int blocks_per_cu) {
 }
 
 
-template <int BM, int BN, int WM, int WN, int ACT>
-void launch_lean(const GemmArgs &g, hipStream_t s) {
+template <int BM, int BN, int WM, int WN, int ACT, int EPI>
+void launch_lean_epi(const GemmArgs &g, hipStream_t s) {
   const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
   constexpr int smem = 2 * (BM + BN) * 128;
   static bool configured = false;
   if (!configured) {
-    set_smem(gemm_lean_kernel<BM, BN, WM, WN, ACT>, smem);
+    set_smem(gemm_lean_kernel<BM, BN, WM, WN, ACT, EPI>, smem);
     configured = true;
   }
-  launch((gemm_lean_kernel<BM, BN, WM, WN, ACT>), dim3(tm * tn), dim3(64 * WM * WN), smem, s, g, tm, tn);
+  launch((gemm_lean_kernel<BM, BN, WM, WN, ACT, EPI>), dim3(tm * tn), dim3(64 * WM * WN), smem, s, g, tm, tn);
+}
+
+template <int BM, int BN, int WM, int WN, int ACT>
+void launch_lean(const GemmArgs &g, hipStream_t s) {
+  switch (g.epi) {
+    case EPI_GEGLU: launch_lean_epi<BM, BN, WM, WN, ACT, EPI_GEGLU>(g, s); break;
+    case EPI_ROPE: launch_lean_epi<BM, BN, WM, WN, ACT, EPI_ROPE>(g, s); break;
+    case EPI_RESADD: launch_lean_epi<BM, BN, WM, WN, ACT, EPI_RESADD>(g, s); break;
+    default: launch_lean_epi<BM, BN, WM, WN, ACT, EPI_NONE>(g, s); break;
+  }
 }
 
 // shapes the lean kernel runs: f16, one matrix, whole 64-wide k slabs, 16-byte output chunks, and
@@ -811,7 +871,8 @@ constexpr int CUS = 256;
 int pick_tile(const GemmArgs &g, bool lean) {
   const char *e = getenv("KH_GEMM_TILE");
   const int forced = e ? atoi(e) : -1;
-  if (forced >= 0 && forced <= 11 && (forced < 8 || lean)) return forced;
+  // (a fused step runs in the lean kernel only)
+  if (forced >= 0 && forced <= 11 && (forced < 8 ? g.epi == EPI_NONE : lean)) return forced;
   // measured on MI355X (f16, random data, encoder shapes M = 13k .. 1.2M): 192x128 leads in
   // general; 192x256 where N is a multiple of 256 and either narrow (N <= 768: one round of tiles
   // at M ~ 13k) or fed by a short K (<= 384, where the epilogue weighs most)
@@ -863,6 +924,22 @@ void launch_mfma(const GemmArgs &g, hipStream_t s) {
 }
 
 }  // namespace
+
+bool gemm_epi_ok(bool f16, const GemmArgs &g) {
+  if (g.epi == EPI_NONE) return true;
+  if (!f16 || !gemm_uses_mfma(f16, g) || !lean_ok(g)) return false;
+  switch (g.epi) {
+    case EPI_GEGLU:  // both halves in one buffer resource; half tiles of whole 16-byte chunks
+      return g.N % 16 == 0 && g.ldc >= g.N / 2 && (int64_t)g.N * g.ldw * 2 < ((int64_t)1 << 31);
+    case EPI_ROPE:  // heads must not straddle tiles (the narrowest tile is 64 columns wide)
+      return g.rope_table && g.row_pos && g.rope_d > 0 && g.rope_d % 16 == 0 && 64 % g.rope_d == 0 &&
+             g.rope_cols <= g.N && g.rope_cols % g.rope_d == 0;
+    case EPI_RESADD:
+      return g.act == 0;
+    default:
+      return false;
+  }
+}
 
 bool gemm_uses_mfma(bool f16, const GemmArgs &g) {
   const int ce = f16 ? 8 : 4;

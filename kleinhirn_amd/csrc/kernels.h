@@ -46,10 +46,23 @@ struct GemmArgs {
   bool c_f32 = false;  // write f32 output whatever the storage type (relative-position scores)
   // force the wavefront-per-output kernel (tests)
   bool rowdot = false;
+  // fused step after the product (f16 lean kernel only; gemm_epi_ok tells when it runs):
+  //  EPI_GEGLU: W holds [a | b] halves of N = 2 I rows; C [M, I] = gelu(a) * b
+  //  EPI_ROPE: rotate-half RoPE on the first rope_cols columns (q and k), head dim rope_d, table
+  //            [L][cos D | sin D] at the row's position row_pos[m]
+  //  EPI_RESADD: C += product (C is the residual stream, updated in place)
+  // each applied to the product rounded to the storage type, as the separate ops read it
+  int epi = 0;
+  const float *rope_table = nullptr;
+  const int32_t *row_pos = nullptr;
+  int rope_cols = 0, rope_d = 0;
 };
+enum { EPI_NONE = 0, EPI_GEGLU = 1, EPI_ROPE = 2, EPI_RESADD = 3 };
 void gemm(bool f16, const GemmArgs &g, hipStream_t s);
 // true when the MFMA tile kernel runs this shape (else the wave-per-output kernel)
 bool gemm_uses_mfma(bool f16, const GemmArgs &g);
+// true when g's fused step (g.epi) can run inside the product for this shape and storage type
+bool gemm_epi_ok(bool f16, const GemmArgs &g);
 
 // Packed-row description of one run: cu[b] .. cu[b+1] are the rows of sequence b.
 struct Packing {

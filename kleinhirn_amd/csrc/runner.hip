@@ -139,6 +139,7 @@ struct Step {
   float eps = 0.f, scale = 1.f;
   bool rel = false;
   std::string markers_id;  // gather: the init buffer holding the markers
+  int epi = 0;             // S_GEMM: fused step (EPI_*); in[4] holds a RoPE table
 };
 
 struct Buffer {
@@ -459,6 +460,93 @@ static void check_bindings(kh_ctx *ctx, const Parsed &pp, const std::vector<Step
   }
 }
 
+
+// ---- fusion of a product with its element-wise consumer ---------------------------------------
+
+// slots a step only writes (its other referenced buffers are read)
+static int write_only_slot(const Step &s) {
+  switch (s.kind) {
+    case S_GEMM: return 3;
+    case S_LN: case S_EMBLN: return 5;
+    case S_GEGLU: case S_ATTN: case S_POOL: case S_GATHER: return 1;
+    default: return -1;  // add and rope update in place: their slot 0 is read too
+  }
+}
+
+// true when no step from `from` on reads buffer `id` before one overwrites it
+static bool dead_after(const std::vector<Step> &steps, size_t from, const std::string &id) {
+  for (size_t i = from; i < steps.size(); i++) {
+    const Step &s = steps[i];
+    const int wo = write_only_slot(s);
+    for (int k = 0; k < 6; k++)
+      if (k != wo && s.in[k].id == id) return false;
+    if (wo >= 0 && s.in[wo].id == id) return true;
+  }
+  return true;
+}
+
+// GEMM + GeGLU, GEMM + RoPE and GEMM + residual add run as one launch when the lean kernel takes
+// the shape (the fused op is applied to the product rounded to the storage type, so results match
+// the separate ops); the intermediate buffer then needs no memory.
+static void fuse_steps(kh_plan *pl) {
+  std::vector<Step> &st = pl->steps;
+  std::vector<Step> out;
+  for (size_t i = 0; i < st.size(); i++) {
+    Step s = st[i];
+    if (s.kind == S_GEMM && !s.seq_rows && i + 1 < st.size()) {
+      const Step &n = st[i + 1];
+      const std::string &c = s.in[3].id;
+      GemmArgs g;
+      g.lda = s.K;
+      g.ldw = s.K;
+      g.ldc = s.N;
+      g.M = 1 << 20;
+      g.N = s.N;
+      g.K = s.K;
+      g.act = s.act;
+      g.a = g.w = (const void *)(uintptr_t)256;  // shape test only: aligned stand-ins
+      Step fused = s;
+      bool ok = false;
+      if (n.kind == S_GEGLU && n.in[0].id == c && 2 * n.I == s.N && c != pl->out_buf && dead_after(st, i + 2, c)) {
+        g.epi = EPI_GEGLU;
+        g.ldc = n.I;
+        if ((ok = gemm_epi_ok(pl->f16, g))) {
+          fused.epi = EPI_GEGLU;
+          fused.in[3] = n.in[1];
+        }
+      } else if (n.kind == S_ROPE && n.in[0].id == c && s.N == 3 * n.H * n.D) {
+        g.epi = EPI_ROPE;
+        g.rope_table = (const float *)(uintptr_t)256;
+        g.row_pos = (const int32_t *)(uintptr_t)256;
+        g.rope_cols = 2 * n.H * n.D;
+        g.rope_d = n.D;
+        if ((ok = gemm_epi_ok(pl->f16, g))) {
+          fused.epi = EPI_ROPE;
+          fused.in[4] = n.in[1];
+          fused.H = n.H;
+          fused.D = n.D;
+        }
+      } else if (n.kind == S_ADD && n.mode == 0 && n.in[1].id == c && n.N == s.N && c != pl->out_buf &&
+                 dead_after(st, i + 2, c)) {
+        g.epi = EPI_RESADD;
+        if ((ok = gemm_epi_ok(pl->f16, g))) {
+          fused.epi = EPI_RESADD;
+          fused.in[3] = n.in[0];
+          fused.name = s.name + "+" + n.name;
+        }
+      }
+      if (ok) {
+        if (fused.epi != EPI_RESADD) fused.name = s.name + "+" + n.name;
+        out.push_back(fused);
+        i++;
+        continue;
+      }
+    }
+    out.push_back(s);
+  }
+  st.swap(out);
+}
+
 // ---- execution ---------------------------------------------------------------------------------
 
 using LaunchHook = std::function<void(const Step &, const char *kernel, double flops, double bytes, bool begin)>;
@@ -491,8 +579,21 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
       g.N = s.N;
       g.K = s.K;
       g.act = s.act;
+      g.epi = s.epi;
+      double out_elems = (double)rows * s.N;  // written (the residual add also reads them)
+      if (s.epi == EPI_GEGLU) {
+        g.ldc = s.N / 2;
+        out_elems = (double)rows * s.N / 2;
+      } else if (s.epi == EPI_ROPE) {
+        g.rope_table = (const float *)bufp(pl, s.in[4]);
+        g.row_pos = pk.row_pos;
+        g.rope_cols = 2 * s.H * s.D;
+        g.rope_d = s.D;
+      } else if (s.epi == EPI_RESADD) {
+        out_elems *= 2;
+      }
       begin(gemm_uses_mfma(f16, g) ? "gemm_mfma" : "gemm_rowdot", 2.0 * rows * s.N * s.K,
-            (double)es * ((double)rows * s.K + (double)s.N * s.K + (double)rows * s.N + (g.bias ? s.N : 0)));
+            (double)es * ((double)rows * s.K + (double)s.N * s.K + out_elems + (g.bias ? s.N : 0)));
       gemm(f16, g, st);
       end();
       break;
@@ -891,6 +992,8 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
   if (inputs.has("markers")) errors.push_back("marker inputs (GLiNER, Julia) are outside the encoder heads");
   if (!errors.empty()) fail(KH_EUNSUPPORTED, join_errors(errors));
   pl->in_emb = inputs.at("embeddings").str();
+  pl->out_buf = pp.root.at("output").at("buffer").str();
+  if (!getenv("KH_NO_FUSION")) fuse_steps(pl.get());
   pl->in_mask = inputs.at("mask").str();
   if (inputs.has("typeIds")) pl->in_tt = inputs.at("typeIds").str();
   const Json &o = pp.root.at("output");

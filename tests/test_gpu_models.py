@@ -98,3 +98,16 @@ def test_device_word_gather_equals_host_gather():
     a = hip_outputs(case, f16=True)
     b = hip_outputs(case, f16=True, by_ids=True)
     assert np.array_equal(a, b)
+
+
+def test_fused_product_steps_match_separate_ops(monkeypatch):
+    """ModernBERT: GEMM + GeGLU, GEMM + RoPE and GEMM + residual add run fused in the product's
+    epilogue; with fusion off (KH_NO_FUSION) the separate kernels run. Both apply the same f32
+    formulas to the same f16 products, so the results are identical."""
+    case, ref = case_and_oracle("c4")
+    fused = hip_outputs(case, f16=True)
+    monkeypatch.setenv("KH_NO_FUSION", "1")
+    separate = hip_outputs(case, f16=True)
+    print(f"fused vs separate: max |d| {np.abs(fused - separate).max():.3e}")
+    assert np.array_equal(fused, separate)
+    assert cosine_rows(ref, fused).min() >= 0.999
