@@ -943,6 +943,10 @@ bool gemm_epi_ok(bool f16, const GemmArgs &g) {
 
 bool gemm_uses_mfma(bool f16, const GemmArgs &g) {
   const int ce = f16 ? 8 : 4;
+  // f32 products too small to fill the chip with 128 x 128 tiles (a short sequence) go to one
+  // wavefront per row and 4 columns instead
+  const int64_t tiles = (int64_t)((g.M + 127) / 128) * ((g.N + 127) / 128) * g.batch;
+  if (!f16 && tiles < 64 && g.epi == EPI_NONE) return false;
   return !g.rowdot && g.N >= 32 && g.K % ce == 0 && g.lda % ce == 0 && g.ldw % ce == 0 && g.a_bs % ce == 0 &&
          g.w_bs % ce == 0 && aligned16(g.a) && aligned16(g.w);
 }
