@@ -78,6 +78,65 @@ __global__ void __launch_bounds__(256) layernorm_kernel(const T *__restrict__ a,
   ln_finish<T, VEC, PER>(v, N, gamma, beta, eps, out + r * N, lane);
 }
 
+
+// Several rows per wavefront: a group of LPR lanes (a power of two) holds one row as PER 16-byte
+// chunks per lane, so every lane loads (a 768-wide f16 row: 32 lanes x 3 chunks, two rows per
+// wavefront) and the reductions stay inside the group.
+template <typename T, int LPR, int PER>
+__global__ void __launch_bounds__(256) layernorm_rows_kernel(const T *__restrict__ a, const T *__restrict__ b,
+                                                             const T *__restrict__ gamma,
+                                                             const T *__restrict__ beta, T *__restrict__ out,
+                                                             int64_t rows, int N, float eps) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int RPW = WAVE / LPR;  // rows per wavefront
+  const int lane = threadIdx.x & 63, l = lane % LPR;
+  const int64_t r = ((int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  if (r >= rows) return;  // whole groups leave together: the shuffles below stay in a group
+  float v[PER][VEC];
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    const int e0 = (k * LPR + l) * VEC;
+    VecIO<T, VEC>::load(a + r * N + e0, v[k]);
+    if (b) {
+      float y[VEC];
+      VecIO<T, VEC>::load(b + r * N + e0, y);
+#pragma unroll
+      for (int i = 0; i < VEC; i++) v[k][i] += y[i];
+    }
+  }
+  auto group_sum = [&](float x) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+  };
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < PER; k++)
+#pragma unroll
+    for (int i = 0; i < VEC; i++) s += v[k][i];
+  const float mean = group_sum(s) / (float)N;
+  float sq = 0.f;
+#pragma unroll
+  for (int k = 0; k < PER; k++)
+#pragma unroll
+    for (int i = 0; i < VEC; i++) {
+      const float d = v[k][i] - mean;
+      sq += d * d;
+    }
+  const float var = group_sum(sq) / (float)N;
+  const float inv = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    const int e0 = (k * LPR + l) * VEC;
+    float gm[VEC], bt[VEC], y[VEC];
+    VecIO<T, VEC>::load(gamma + e0, gm);
+    if (beta) VecIO<T, VEC>::load(beta + e0, bt);
+#pragma unroll
+    for (int i = 0; i < VEC; i++) y[i] = (v[k][i] - mean) * inv * gm[i] + (beta ? bt[i] : 0.f);
+    VecIO<T, VEC>::store(out + r * N + e0, y);
+  }
+}
+
 // word + position + type in f32 ((word + pos) + type), then LayerNorm (src/wasm/plan.ts:433-447).
 // Position row: tt >> 16 with POSIDS, else the row's position in its sequence + OFFSET, clamped to
 // MAXPOS - 1. Type row: tt & 0xffff.
@@ -139,6 +198,24 @@ bool dispatch_per(int N, F &&f) {
 template <typename T>
 void layernorm_t(const void *a, const void *b, const void *gamma, const void *beta, void *out, int64_t rows,
                  int N, float eps, hipStream_t s) {
+  // rows of 3 x 2^j 16-byte chunks (384- and 768-wide f16, 384-wide f32): groups of 2^j lanes
+  constexpr int VEC16 = 16 / sizeof(T);
+  if (N % (3 * VEC16) == 0) {
+    const int lpr = N / (3 * VEC16);
+    auto go_rows = [&](auto lpr_t) {
+      constexpr int LPR = decltype(lpr_t)::value;
+      const int64_t per_block = (int64_t)ROWS_PER_BLOCK * (WAVE / LPR);
+      launch((layernorm_rows_kernel<T, LPR, 3>), dim3((unsigned)((rows + per_block - 1) / per_block)), dim3(256),
+             0, s, (const T *)a, (const T *)b, (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps);
+    };
+    switch (lpr) {
+      case 8: go_rows(std::integral_constant<int, 8>()); return;
+      case 16: go_rows(std::integral_constant<int, 16>()); return;
+      case 32: go_rows(std::integral_constant<int, 32>()); return;
+      case 64: go_rows(std::integral_constant<int, 64>()); return;
+      default: break;
+    }
+  }
   dim3 grid((unsigned)((rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK));
   auto go = [&](auto vec) {
     constexpr int VEC = decltype(vec)::value;

@@ -121,8 +121,9 @@ def test_matmul_every_tile_configuration(tile, monkeypatch):
 
 
 @pytest.mark.parametrize("f16", [False, True])
-def test_layernorm_modes_and_embln(f16):
-    N = 384
+@pytest.mark.parametrize("N", [384, 768, 40])
+def test_layernorm_modes_and_embln(f16, N):
+    """384 and 768: several rows per wavefront (lane groups); 40: one wavefront per row."""
     L, lens = 9, [4, 9]
     B = len(lens)
     dt = np.float16 if f16 else np.float32
