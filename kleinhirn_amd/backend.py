@@ -112,12 +112,16 @@ class HipPlanRunner:
         _check(lib().kh_plan_create(backend.ctx, doc, len(doc), ctypes.byref(h)))
         self.h = h
         for bid, raw in plan_inits(plan).items():
-            buf = np.frombuffer(raw, dtype=np.uint8)
-            _check(lib().kh_plan_init_buffer(self.h, bid.encode(), _ptr(buf), buf.nbytes))
+            self.init_buffer(bid, raw)
         self.length = plan["length"]
         self.batch = plan["batch"]
         self.markers = plan["markers"]
         self._keep = None
+
+    def init_buffer(self, bid: str, raw: bytes | np.ndarray) -> None:
+        """BufferDecl.init of one buffer (src/plan/executor.ts:118-124)."""
+        buf = np.ascontiguousarray(np.frombuffer(bytes(raw), dtype=np.uint8))
+        _check(lib().kh_plan_init_buffer(self.h, bid.encode(), _ptr(buf), buf.nbytes))
 
     @property
     def info(self) -> PlanInfo:

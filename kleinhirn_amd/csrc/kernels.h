@@ -129,6 +129,10 @@ void attention(bool f16, const AttnArgs &a, const Packing &p, hipStream_t s);
 constexpr int ATTN_QTILE = 64;
 constexpr int ATTN_REL_LMAX = 512;  // longest plan the relative attention kernel takes
 
+// Row 0 of each sequence into one row per sequence (from_packed), or one row per sequence copied
+// with empty sequences zeroed; rows of width D.
+void first_rows(bool f16, const void *src, void *dst, int D, bool from_packed, const Packing &p, hipStream_t s);
+
 // Convert storage rows to f32 (readback of f16 outputs).
 void to_f32(bool f16, const void *src, float *dst, int64_t n, hipStream_t s);
 

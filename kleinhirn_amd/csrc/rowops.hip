@@ -3,6 +3,8 @@
 // One 64-lane wavefront per row for the normalisations: the row stays in registers between the
 // mean and the variance pass (variance = mean((v - mean)^2), the reference's two-pass form,
 // src/wasm/plan.ts:386-411), loads are VEC-wide and coalesced across the wavefront.
+#include <algorithm>
+
 #include "kernels.h"
 #include "device.h"
 
@@ -367,6 +369,21 @@ __global__ void __launch_bounds__(256) gather_kernel(const T *__restrict__ x, co
   }
 }
 
+// Row 0 of each sequence between the packed rows and one row per sequence (compact): packed ->
+// compact copies row cu[b], compact -> compact copies row b; empty sequences give zeros (as the
+// row gather of a pooled head reads them).
+template <typename T>
+__global__ void __launch_bounds__(256) first_rows_kernel(const T *__restrict__ src, T *__restrict__ dst, int D, int B,
+                                                         const int32_t *__restrict__ cu, int from_packed) {
+  const int64_t total = (int64_t)B * D;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int b = (int)(i / D), d = (int)(i - (int64_t)b * D);
+    const int64_t row = from_packed ? cu[b] : b;
+    dst[i] = cu[b + 1] > cu[b] ? src[row * D + d] : (T)0.f;
+  }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(256) to_f32_kernel(const T *__restrict__ src, float *__restrict__ dst, int64_t n) {
   int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -381,6 +398,16 @@ unsigned grid_for(int64_t n, int per_thread = 1) {
 }
 
 }  // namespace
+
+void first_rows(bool f16, const void *src, void *dst, int D, bool from_packed, const Packing &p, hipStream_t s) {
+  const int64_t total = (int64_t)p.B * D;
+  if (total <= 0) return;
+  const dim3 grid((unsigned)std::min<int64_t>((total + 255) / 256, 4096));
+  if (f16) launch((first_rows_kernel<half_t>), grid, dim3(256), 0, s, (const half_t *)src, (half_t *)dst, D, p.B, p.cu,
+                  (int)from_packed);
+  else launch((first_rows_kernel<float>), grid, dim3(256), 0, s, (const float *)src, (float *)dst, D, p.B, p.cu,
+              (int)from_packed);
+}
 
 void layernorm(bool f16, const void *a, const void *b, const void *gamma, const void *beta, void *out,
                int64_t rows, int N, float eps, hipStream_t s) {

@@ -120,7 +120,7 @@ struct kh_ctx {
 
 namespace kh {
 
-enum StepKind { S_EMBLN, S_LN, S_GEMM, S_ADD, S_GEGLU, S_ROPE, S_ATTN, S_POOL, S_GATHER };
+enum StepKind { S_EMBLN, S_LN, S_GEMM, S_ADD, S_GEGLU, S_ROPE, S_ATTN, S_POOL, S_GATHER, S_COMPACT };
 
 // A buffer reference of a step: device pointer resolved at plan creation.
 struct Ref {
@@ -140,6 +140,7 @@ struct Step {
   bool rel = false;
   std::string markers_id;  // gather: the init buffer holding the markers
   int epi = 0;             // S_GEMM: fused step (EPI_*); in[4] holds a RoPE table
+  bool first_tiles = false;  // S_ATTN: only the first query tile of each sequence
 };
 
 struct Buffer {
@@ -164,6 +165,12 @@ struct kh_plan {
   int L = 0, B = 0, markers = 0, E = 0;
   std::map<std::string, Buffer> bufs;
   std::vector<Step> steps;
+  // the same forward with the tail after the last attention on one row per sequence (empty when the
+  // plan has no such tail); it runs while every marker of the head's row gather is 0
+  std::vector<Step> steps_pruned;
+  std::string prune_markers;
+  std::vector<uint8_t> markers_shadow;  // host copy of that markers buffer
+  bool markers_first = true;
   std::string in_emb, in_mask, in_tt;
   std::string out_buf;
   int out_rows = 0, out_cols = 0;
@@ -184,17 +191,21 @@ struct kh_plan {
   // packing of the current upload
   std::vector<int32_t> cu;
   int64_t T = 0;
-  int ntiles = 0;
+  int ntiles = 0, ntiles_first = 0;
   double attn_pairs_global = 0;  // sum over sequences of n^2
   std::map<int, double> attn_pairs_window;  // window -> sum of visited (i, j) pairs
+  double attn_pairs_first = 0;  // the same for the first query tile of each sequence
+  std::map<int, double> attn_pairs_first_window;
+  int64_t rows_first = 0;  // query rows of the first tiles
   HostPinned pin_emb, pin_meta;
-  DevMem d_cu, d_row_pos, d_row_seq, d_tiles, d_tt, d_ids;
+  DevMem d_cu, d_row_pos, d_row_seq, d_tiles, d_tiles_first, d_tt, d_ids;
 
   // relative attention
   std::vector<int32_t> bucket_host;
   DevMem d_bucket;
   int rel_nb = 0;
   double rel_rows_buckets = 0;  // sum over sequences of rows x buckets reached (c2p + p2c work)
+  double rel_rows_buckets_first = 0;
 
   // cos/sin tables (f32)
   std::map<std::string, std::unique_ptr<DevMem>> tables;
@@ -468,7 +479,7 @@ static int write_only_slot(const Step &s) {
   switch (s.kind) {
     case S_GEMM: return 3;
     case S_LN: case S_EMBLN: return 5;
-    case S_GEGLU: case S_ATTN: case S_POOL: case S_GATHER: return 1;
+    case S_GEGLU: case S_ATTN: case S_POOL: case S_GATHER: case S_COMPACT: return 1;
     default: return -1;  // add and rope update in place: their slot 0 is read too
   }
 }
@@ -547,6 +558,164 @@ static void fuse_steps(kh_plan *pl) {
   st.swap(out);
 }
 
+// ---- one row per sequence after the last attention ----------------------------------------------
+
+// Row buffers a row-local step reads and writes, with their row widths (elements). False for a
+// step that is not row-local over the packed rows, or that takes a buffer as its weight.
+struct RowUse {
+  int slot, width;
+  bool read, write;
+};
+static bool row_uses(const Step &s, std::vector<RowUse> &u) {
+  u.clear();
+  auto is_w = [](const std::string &id) { return id.rfind("w:", 0) == 0 || id == "zero" || id == "dummy"; };
+  if (s.seq_rows) return false;
+  switch (s.kind) {
+    case S_GEMM:
+      if (s.epi == EPI_ROPE || !is_w(s.in[1].id) || !is_w(s.in[2].id)) return false;
+      u.push_back({0, s.K, true, false});
+      u.push_back({3, s.epi == EPI_GEGLU ? s.N / 2 : s.N, s.epi == EPI_RESADD, true});
+      return true;
+    case S_LN:
+      u.push_back({0, s.N, true, false});
+      if (s.mode == 2) u.push_back({1, s.N, true, false});
+      u.push_back({5, s.N, false, true});
+      return true;
+    case S_ADD:
+      if (s.mode != 0) return false;
+      u.push_back({1, s.N, true, false});
+      u.push_back({0, s.N, true, true});
+      return true;
+    case S_GEGLU:
+      u.push_back({0, 2 * s.I, true, false});
+      u.push_back({1, s.I, false, true});
+      return true;
+    default:
+      return false;
+  }
+}
+
+// A pooled-CLS head gathers one row per sequence (pool 'cls' -> gather 'first' with K = 1,
+// src/plan/build.ts:303-310): after the last attention only row 0 of each sequence reaches the
+// output. The steps between that attention and the gather are row-local, so they run on B rows
+// ("id@cls" buffers, one row per sequence) instead of T, the last attention computes only the first
+// query tile of each sequence, and the gather becomes a copy of the B rows that zeroes empty
+// sequences (as the gather does). Products and LayerNorms treat every row alike, so the B rows
+// equal the full computation's row 0 of each sequence.
+static void prune_tail(kh_plan *pl) {
+  const std::vector<Step> &st = pl->steps;
+  int g = -1, a = -1;
+  for (int i = 0; i < (int)st.size(); i++) {
+    if (st[i].kind == S_GATHER || st[i].kind == S_POOL) {
+      if (g >= 0) return;
+      g = i;
+    }
+  }
+  if (g < 0 || st[g].kind != S_GATHER || st[g].Kmk != 1) return;
+  for (int i = 0; i < g; i++)
+    if (st[i].kind == S_ATTN) a = i;
+  if (a < 0) return;
+  const int B = pl->B;
+  const size_t es = pl->f16 ? 2 : 4;
+  auto cls = [](const std::string &id) { return id + "@cls"; };
+  std::map<std::string, int> width;      // tail buffer -> widest row it holds
+  std::vector<std::pair<std::string, int>> live_in;  // read before the tail writes them
+  std::set<std::string> written;
+  std::vector<RowUse> u;
+  std::vector<Step> tail;
+  for (int i = a + 1; i < g; i++) {
+    if (!row_uses(st[i], u)) return;
+    Step t = st[i];
+    for (const RowUse &r : u) {
+      const std::string &id = st[i].in[r.slot].id;
+      if (!pl->bufs.count(id) || id == pl->out_buf) return;
+      if (r.read && !written.count(id)) {
+        bool seen = false;
+        for (auto &li : live_in) seen = seen || li.first == id;
+        if (!seen) live_in.push_back({id, r.width});
+      }
+      width[id] = std::max(width[id], r.width);
+      t.in[r.slot].id = cls(id);
+    }
+    for (const RowUse &r : u)
+      if (r.write) written.insert(st[i].in[r.slot].id);
+    t.seq_rows = true;
+    t.rows_fixed = B;
+    tail.push_back(std::move(t));
+  }
+  // the gather reads one row of width D per sequence
+  const Step &gs = st[g];
+  const std::string &src = gs.in[0].id;
+  if (!pl->bufs.count(src) || !pl->bufs.count(gs.in[1].id)) return;
+  if (!written.count(src)) {
+    bool seen = false;
+    for (auto &li : live_in) seen = seen || li.first == src;
+    if (!seen) live_in.push_back({src, gs.D});
+  }
+  width[src] = std::max(width[src], gs.D);
+  // head steps after the gather work on sequence rows and touch no buffer of the tail
+  for (int i = g + 1; i < (int)st.size(); i++) {
+    if (!st[i].seq_rows || st[i].kind == S_ATTN || st[i].kind == S_GATHER) return;
+    for (const Ref &r : st[i].in)
+      if (width.count(r.id)) return;
+  }
+  for (const auto &li : live_in) {
+    const Buffer &b = pl->bufs.at(li.first);
+    if (b.bytes < (int64_t)pl->L * B * li.second * (int64_t)es) return;  // not a [L * B, width] row buffer
+  }
+
+  std::vector<Step> out(st.begin(), st.begin() + a);
+  Step at = st[a];
+  at.first_tiles = true;
+  out.push_back(at);
+  for (const auto &li : live_in) {
+    Step c;
+    c.kind = S_COMPACT;
+    c.name = "compact " + li.first;
+    c.in[0].id = li.first;
+    c.in[1].id = cls(li.first);
+    c.D = width.at(li.first);
+    c.mode = 1;
+    c.seq_rows = true;
+    out.push_back(c);
+  }
+  for (Step &t : tail) out.push_back(std::move(t));
+  Step c;
+  c.kind = S_COMPACT;
+  c.name = gs.name;
+  c.in[0].id = cls(src);
+  c.in[1].id = gs.in[1].id;
+  c.D = gs.D;
+  c.mode = 0;
+  c.seq_rows = true;
+  out.push_back(c);
+  for (int i = g + 1; i < (int)st.size(); i++) out.push_back(st[i]);
+  for (const auto &w : width) {
+    Buffer b;
+    b.bytes = ((int64_t)B * w.second * (int64_t)es + 255) & ~(int64_t)255;
+    b.usage = "rw";
+    pl->bufs.emplace(cls(w.first), std::move(b));
+  }
+  pl->steps_pruned.swap(out);
+  pl->prune_markers = gs.markers_id;
+}
+
+// The pruned list is valid while the gather takes row 0 of every sequence (marker b * 3 is 0).
+static void check_markers(kh_plan *pl) {
+  const std::vector<uint8_t> &m = pl->markers_shadow;
+  bool first = (size_t)pl->B * 3 * 4 <= m.size();
+  for (int b = 0; first && b < pl->B; b++) {
+    uint32_t v;
+    memcpy(&v, m.data() + (size_t)b * 12, 4);
+    first = v == 0;
+  }
+  pl->markers_first = first;
+}
+
+static const std::vector<Step> &active_steps(const kh_plan *pl) {
+  return !pl->steps_pruned.empty() && pl->markers_first ? pl->steps_pruned : pl->steps;
+}
+
 // ---- execution ---------------------------------------------------------------------------------
 
 using LaunchHook = std::function<void(const Step &, const char *kernel, double flops, double bytes, bool begin)>;
@@ -558,7 +727,8 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
   const bool f16 = pl->f16;
   const size_t es = f16 ? 2 : 4;
   const Packing pk = packing_of(pl);
-  const int64_t rows = s.seq_rows ? (s.kind == S_POOL || s.kind == S_GATHER ? pl->B : s.rows_fixed) : pl->T;
+  const int64_t rows =
+      s.seq_rows ? (s.kind == S_POOL || s.kind == S_GATHER || s.kind == S_COMPACT ? pl->B : s.rows_fixed) : pl->T;
   auto begin = [&](const char *k, double fl, double by) {
     if (hook) hook(s, k, fl, by, true);
   };
@@ -629,13 +799,18 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
       break;
     }
     case S_ADD:
-      begin("add", (double)pl->T * s.N, 3.0 * es * pl->T * s.N);
-      add(f16, bufp(pl, s.in[0]), bufp(pl, s.in[1]), pl->T, s.N, s.mode, pk, st);
+      begin("add", (double)rows * s.N, 3.0 * es * rows * s.N);
+      add(f16, bufp(pl, s.in[0]), bufp(pl, s.in[1]), rows, s.N, s.mode, pk, st);
       end();
       break;
     case S_GEGLU:
-      begin("geglu", 20.0 * pl->T * s.I, 3.0 * es * pl->T * s.I);
-      geglu(f16, bufp(pl, s.in[0]), bufp(pl, s.in[1]), pl->T, s.I, st);
+      begin("geglu", 20.0 * rows * s.I, 3.0 * es * rows * s.I);
+      geglu(f16, bufp(pl, s.in[0]), bufp(pl, s.in[1]), rows, s.I, st);
+      end();
+      break;
+    case S_COMPACT:
+      begin("compact", 0, 2.0 * es * pl->B * s.D);
+      first_rows(f16, bufp(pl, s.in[0]), bufp(pl, s.in[1]), s.D, s.mode == 1, pk, st);
       end();
       break;
     case S_ROPE: {
@@ -666,11 +841,13 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
       a.D = s.D;
       a.scale = s.scale;
       a.window = s.window;
-      a.tiles = (const int2 *)pl->d_tiles.p;
-      a.ntiles = pl->ntiles;
+      a.tiles = (const int2 *)(s.first_tiles ? pl->d_tiles_first.p : pl->d_tiles.p);
+      a.ntiles = s.first_tiles ? pl->ntiles_first : pl->ntiles;
       const double hd = (double)s.H * s.D;
-      double pairs = pl->attn_pairs_global;
-      if (s.window > 0) pairs = pl->attn_pairs_window[s.window];
+      double pairs = s.first_tiles ? pl->attn_pairs_first : pl->attn_pairs_global;
+      if (s.window > 0) pairs = (s.first_tiles ? pl->attn_pairs_first_window : pl->attn_pairs_window)[s.window];
+      // q and ctx rows of the computed tiles, k and v of every row
+      const double io_rows = s.first_tiles ? 2.0 * pl->T + 2.0 * pl->rows_first : 4.0 * pl->T;
       double rel_fl = 0;
       if (s.rel) {
         // q . pos_key[m] and k . pos_query[m] over the buckets each sequence reaches, inside the kernel
@@ -679,9 +856,9 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
         a.bucket = (const int32_t *)pl->d_bucket.p;
         a.nb = pl->rel_nb;
         a.lmax = pl->L;
-        rel_fl = 4.0 * hd * pl->rel_rows_buckets;
+        rel_fl = 4.0 * hd * (s.first_tiles ? pl->rel_rows_buckets_first : pl->rel_rows_buckets);
       }
-      begin(s.rel ? "attention_rel" : "attention", 4.0 * hd * pairs + rel_fl, (double)es * 4.0 * pl->T * hd);
+      begin(s.rel ? "attention_rel" : "attention", 4.0 * hd * pairs + rel_fl, (double)es * io_rows * hd);
       attention(f16, a, pk, st);
       end();
       break;
@@ -718,35 +895,51 @@ static void pack(kh_plan *pl, int rows) {
   std::vector<int32_t> row_pos(T > 0 ? T : 1), row_seq(T > 0 ? T : 1);
   std::vector<int2> tiles;
   pl->attn_pairs_global = 0;
+  std::vector<int2> tiles_first;
   std::set<int> windows;
   for (const Step &s : pl->steps)
     if (s.kind == S_ATTN && s.window > 0) windows.insert(s.window);
   pl->attn_pairs_window.clear();
+  pl->attn_pairs_first = 0;
+  pl->attn_pairs_first_window.clear();
+  pl->rows_first = 0;
   for (int b = 0; b < B; b++) {
     for (int i = 0; i < n[b]; i++) {
       row_pos[pl->cu[b] + i] = i;
       row_seq[pl->cu[b] + i] = b;
     }
     for (int q = 0; q < n[b]; q += ATTN_QTILE) tiles.push_back(make_int2(b, q));
+    const int nq = std::min(n[b], ATTN_QTILE);
+    if (n[b] > 0) tiles_first.push_back(make_int2(b, 0));
+    pl->rows_first += nq;
     pl->attn_pairs_global += (double)n[b] * n[b];
+    pl->attn_pairs_first += (double)nq * n[b];
     for (int w : windows) {
-      double s = 0;
+      double s = 0, s1 = 0;
       for (int i = 0; i < n[b]; i++) {
         const int lo = std::max(0, i - w), hi = std::min(n[b] - 1, i + w);
         s += hi - lo + 1;
+        if (i < nq) s1 += hi - lo + 1;
       }
       pl->attn_pairs_window[w] += s;
+      pl->attn_pairs_first_window[w] += s1;
     }
   }
   pl->ntiles = (int)tiles.size();
+  pl->ntiles_first = (int)tiles_first.size();
   pl->rel_rows_buckets = 0;
+  pl->rel_rows_buckets_first = 0;
   if (!pl->bucket_host.empty())
     for (int b = 0; b < B; b++)
-      if (n[b] > 0)
+      if (n[b] > 0) {
         // buckets are monotone in i - j: those of distances -(n - 1) .. n - 1 form one range
-        pl->rel_rows_buckets += (double)n[b] * (pl->bucket_host[(L - 1) + (n[b] - 1)] -
-                                                pl->bucket_host[(L - 1) - (n[b] - 1)] + 1);
+        const double range = pl->bucket_host[(L - 1) + (n[b] - 1)] - pl->bucket_host[(L - 1) - (n[b] - 1)] + 1;
+        pl->rel_rows_buckets += (double)n[b] * range;
+        // first tile: c2p over its query rows, p2c over every key row
+        pl->rel_rows_buckets_first += 0.5 * (std::min(n[b], ATTN_QTILE) + n[b]) * range;
+      }
   if (tiles.empty()) tiles.push_back(make_int2(0, 0));
+  if (tiles_first.empty()) tiles_first.push_back(make_int2(0, 0));
 
   // metadata: cu | row_pos | row_seq | tiles | tt | ids, one pinned staging block
   const size_t es = pl->f16 ? 2 : 4;
@@ -754,10 +947,13 @@ static void pack(kh_plan *pl, int rows) {
   if (pl->d_row_pos.bytes < (size_t)T * 4 || !pl->d_row_pos.p) pl->d_row_pos.alloc(std::max<int64_t>(T, 1) * 4);
   if (pl->d_row_seq.bytes < (size_t)T * 4 || !pl->d_row_seq.p) pl->d_row_seq.alloc(std::max<int64_t>(T, 1) * 4);
   if (pl->d_tiles.bytes < tiles.size() * sizeof(int2) || !pl->d_tiles.p) pl->d_tiles.alloc(tiles.size() * sizeof(int2));
+  if (pl->d_tiles_first.bytes < tiles_first.size() * sizeof(int2) || !pl->d_tiles_first.p)
+    pl->d_tiles_first.alloc(tiles_first.size() * sizeof(int2));
   KH_CHECK(hipStreamSynchronize(pl->stream));  // staging may still feed an earlier copy
-  // six blocks at most (cu, row_pos, row_seq, tiles, type ids, ids), each 16-byte aligned
+  // seven blocks at most (cu, row_pos, row_seq, tiles, first tiles, type ids, ids), each 16-byte aligned
   const size_t T1 = (size_t)std::max<int64_t>(T, 1);
-  const size_t meta = (size_t)(B + 1) * 4 + 4 * T1 * 4 + tiles.size() * sizeof(int2) + 6 * 16;
+  const size_t meta =
+      (size_t)(B + 1) * 4 + 4 * T1 * 4 + (tiles.size() + tiles_first.size()) * sizeof(int2) + 7 * 16;
   pl->pin_meta.ensure(meta);
   char *mp = (char *)pl->pin_meta.p;
   char *const mend = mp + meta;
@@ -771,6 +967,7 @@ static void pack(kh_plan *pl, int rows) {
   put(pl->d_row_pos, row_pos.data(), (size_t)std::max<int64_t>(T, 1) * 4);
   put(pl->d_row_seq, row_seq.data(), (size_t)std::max<int64_t>(T, 1) * 4);
   put(pl->d_tiles, tiles.data(), tiles.size() * sizeof(int2));
+  put(pl->d_tiles_first, tiles_first.data(), tiles_first.size() * sizeof(int2));
   // packed type ids
   if (!pl->in_tt.empty()) {
     // type rows the embedding reads must exist (an out-of-range id would read past the table)
@@ -829,7 +1026,7 @@ static void ensure_rel(kh_plan *pl) {
 }
 
 static void run_steps(kh_plan *pl, const LaunchHook &hook) {
-  for (const Step &s : pl->steps) exec_step(pl, s, hook);
+  for (const Step &s : active_steps(pl)) exec_step(pl, s, hook);
   KH_CHECK(hipGetLastError());
 }
 
@@ -1008,9 +1205,14 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
     buf.usage = b.at("usage").str();
     pl->bufs.emplace(b.at("id").str(), std::move(buf));
   }
+  if (!getenv("KH_NO_PRUNE")) prune_tail(pl.get());
   // row spaces and uses
   pl->bufs.at(pl->in_emb).packed_space = true;
-  for (Step &s : pl->steps) {
+  std::vector<Step *> all_steps;
+  for (Step &s : pl->steps) all_steps.push_back(&s);
+  for (Step &s : pl->steps_pruned) all_steps.push_back(&s);
+  for (Step *sp : all_steps) {
+    Step &s = *sp;
     for (Ref &r : s.in) {
       if (r.id.empty() || r.id.rfind("w:", 0) == 0 || r.id == "zero" || r.id == "dummy") continue;
       pl->bufs.at(r.id).used = true;
@@ -1025,6 +1227,7 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
       case S_ATTN: dst = &s.in[1].id; break;
       case S_POOL: dst = &s.in[1].id; break;
       case S_GATHER: dst = &s.in[1].id; break;
+      case S_COMPACT: dst = &s.in[1].id; break;
       default: break;
     }
     if (dst) {
@@ -1038,8 +1241,14 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
   pl->bufs.at(pl->in_emb).used = true;
   pl->out_packed = pl->bufs.at(pl->out_buf).packed_space;
   // in-place kernels read what their destination held: the residual stream of a pre-norm layer
-  for (Step &s : pl->steps)
-    if ((s.kind == S_ADD || s.kind == S_ROPE) && pl->bufs.count(s.in[0].id)) pl->bufs.at(s.in[0].id).packed_space = true;
+  for (Step *s : all_steps)
+    if ((s->kind == S_ADD || s->kind == S_ROPE) && !s->seq_rows && pl->bufs.count(s->in[0].id))
+      pl->bufs.at(s->in[0].id).packed_space = true;
+  if (!pl->prune_markers.empty()) {
+    const Buffer &mb = pl->bufs.at(pl->prune_markers);
+    pl->markers_shadow.assign((size_t)mb.bytes, 0);  // device copy starts zeroed
+    check_markers(pl.get());
+  }
 
   KH_CHECK(hipSetDevice(ctx->device));
   KH_CHECK(hipStreamCreateWithFlags(&pl->stream, hipStreamNonBlocking));
@@ -1056,7 +1265,8 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
     KH_CHECK(hipMemset(b.mem->p, 0, (size_t)b.bytes));
   }
   // resolve step pointers
-  for (Step &s : pl->steps) {
+  for (Step *sp : all_steps) {
+    Step &s = *sp;
     for (Ref &r : s.in) {
       if (r.id.empty()) continue;
       if (r.id == "zero" || r.id == "dummy") {
@@ -1117,6 +1327,10 @@ int kh_plan_init_buffer(kh_plan *plan, const char *id, const void *data, size_t 
     return KH_OK;
   }
   if (b.mem) KH_CHECK(hipMemcpy(b.mem->p, data, bytes, hipMemcpyHostToDevice));
+  if (sid == plan->prune_markers) {
+    memcpy(plan->markers_shadow.data(), data, bytes);
+    check_markers(plan);
+  }
   KH_API_END
 }
 
@@ -1135,9 +1349,7 @@ int kh_plan_info_get(const kh_plan *plan, kh_plan_info *out) {
   out->bytes = bytes;
   out->out_rows = plan->out_rows;
   out->out_cols = plan->out_cols;
-  int launches = 0;
-  for (const Step &s : plan->steps) launches += (s.kind == S_ATTN && s.rel) ? 3 : 1;
-  out->launches = launches;
+  out->launches = (int32_t)active_steps(plan).size();
   KH_API_END
 }
 

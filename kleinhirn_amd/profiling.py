@@ -34,6 +34,7 @@ FAMILIES = [
     ("rope_kernel", "rope"),
     ("pool_kernel", "pool"),
     ("gather_kernel", "gather"),
+    ("first_rows_kernel", "compact"),
     ("to_f32_kernel", "to_f32"),
     ("elementwise_kernel", "probe_copy"),
     ("copyBuffer", "runtime_copy"),

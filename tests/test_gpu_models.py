@@ -12,6 +12,8 @@ import os
 import numpy as np
 import pytest
 
+from kleinhirn_amd import configs, inputs
+from kleinhirn_amd.plan.build import build_plan
 from tests.helpers import cosine_rows, decision_parity, hip_outputs, oracle_outputs, workload_case
 
 pytestmark = pytest.mark.gpu
@@ -111,3 +113,62 @@ def test_fused_product_steps_match_separate_ops(monkeypatch):
     print(f"fused vs separate: max |d| {np.abs(fused - separate).max():.3e}")
     assert np.array_equal(fused, separate)
     assert cosine_rows(ref, fused).min() >= 0.999
+
+
+@pytest.mark.parametrize("key", ["c2", "c3b", "c4", "c5"])
+def test_cls_tail_on_sequence_rows_equals_full_forward(monkeypatch, key):
+    """A pooled-CLS head reads row 0 of each sequence after the last attention, so the runner runs
+    the rest of the encoder on one row per sequence (and the last attention on each sequence's
+    first query tile); with KH_NO_PRUNE every row runs. The kept rows go through the same f16
+    kernels in the same accumulation order, so the outputs are identical."""
+    case, ref = case_and_oracle(key)
+    pruned = hip_outputs(case, f16=True)
+    monkeypatch.setenv("KH_NO_PRUNE", "1")
+    full = hip_outputs(case, f16=True)
+    print(f"{key} pruned vs full: max |d| {np.abs(pruned - full).max():.3e}")
+    assert np.array_equal(pruned, full)
+
+
+def test_cls_tail_f32_matches_full_forward_and_oracle(monkeypatch):
+    """f32: the B-row products of the pruned tail are too small for the MFMA tiles and run on the
+    wavefront-per-output kernel (another summation order), so the bar is the f32 parity bar."""
+    case, ref = case_and_oracle("c2")
+    pruned = hip_outputs(case, f16=False)
+    monkeypatch.setenv("KH_NO_PRUNE", "1")
+    full = hip_outputs(case, f16=False)
+    print(f"c2 f32 pruned vs full: max |d| {np.abs(pruned - full).max():.3e}")
+    assert np.abs(pruned - full).max() <= 1e-4
+    check_f32("c2", ref, pruned)
+
+
+def test_cls_tail_with_empty_sequences_and_moved_markers(monkeypatch):
+    """Sequences cut to 0 rows by the run's row count gather zero states in both forms; a marker
+    other than row 0 switches the runner back to the full forward (the gather then reads that row)."""
+    from kleinhirn_amd.backend import HipBackend
+    case, _ = case_and_oracle("c2")
+    W = configs.storage(case.weights, True)
+    be = HipBackend(W)
+    table = W["embeddings.word.weight"]
+    B, L = len(case.ids), case.length
+    plan = build_plan(case.spec, case.head, L, B, True)
+    rows = L * (B - 2) + 5  # sequence B - 2 keeps at most 5 rows, sequence B - 1 none
+
+    def run(markers=None):
+        r = be.runner(plan)
+        if markers is not None:
+            r.init_buffer("first", markers.tobytes())
+        r.upload(inputs.run_input(case.spec, table, case.ids, L))
+        r.run(rows)
+        out = r.read_output().reshape(B, -1)
+        r.destroy()
+        return out
+
+    moved = np.zeros(3 * B, dtype=np.uint32)
+    moved[3 * 1] = 2  # sequence 1 takes its row 2
+    pruned, pruned_moved = run(), run(moved)
+    monkeypatch.setenv("KH_NO_PRUNE", "1")
+    full, full_moved = run(), run(moved)
+    assert np.array_equal(pruned, full)
+    assert np.array_equal(pruned_moved, full_moved)
+    assert not np.array_equal(pruned_moved[1], pruned[1])
+    assert np.array_equal(np.delete(pruned_moved, 1, axis=0), np.delete(pruned, 1, axis=0))
