@@ -596,7 +596,7 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
   constexpr int GROUPS = (BM + BN) / 8;
   constexpr int P = GROUPS / NW;
   static_assert(P * NW == GROUPS, "row groups must split evenly over the wavefronts");
-  static_assert((BN & (BN - 1)) == 0, "the epilogue's chunk rotation needs a power-of-two BN");
+  static_assert(BN % 64 == 0, "whole 64-column MFMA pairs per tile");
   static_assert(BM * BN * 2 <= 2 * (BM + BN) * 128, "the output tile must fit the slab ring");
   constexpr int STAGE = (BM + BN) * 128;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
@@ -713,14 +713,14 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
         half4v o;
 #pragma unroll
         for (int e = 0; e < 4; e++) o[e] = (half_t)act_fn<ACT>(acc[i][j][4 * q + e] + b[e]);
-        const int chunk = ((nl >> 3) + ml) & (CPR - 1);
+        const int chunk = ((nl >> 3) + ml) % CPR;
         *reinterpret_cast<half4v *>(smem + ml * RB + chunk * 16 + lg * 8) = o;
       }
     }
   __syncthreads();
   half_t *C = (half_t *)g.c;
   auto chunk_at = [&](int row, int cc) {
-    return *reinterpret_cast<const half8v *>(smem + row * RB + ((cc + row) & (CPR - 1)) * 16);
+    return *reinterpret_cast<const half8v *>(smem + row * RB + ((cc + row) % CPR) * 16);
   };
   if constexpr (EPI == EPI_GEGLU) {
     // output columns n0 / 2 .. n0 / 2 + BN / 2 of C [M, N / 2]: gelu(a) * b, a and b as stored
@@ -863,8 +863,16 @@ void launch_reg(const GemmArgs &g, hipStream_t s) {
 
 constexpr int CUS = 256;
 
+// Per-CU work of a lean configuration: the tiles the busiest CU runs times the tile's area (a
+// launch of 258 tiles of 192 x 256 on 256 CUs takes two rounds, as long as 512 such tiles).
+static int64_t lean_cost(const GemmArgs &g, int bm, int bn) {
+  const int64_t tiles = (int64_t)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
+  return (tiles + CUS - 1) / CUS * bm * bn;
+}
+
 // Tile configurations. Lean f16 kernel: 8 = 192x128 (4 wavefronts of 96x64, two blocks per CU),
-// 9 = 192x256 (8 wavefronts of 96x64), 10 = 128x128 (4 of 64x64), 11 = 64x64 (1). DMA kernel: 0 = 256x256 (8 of
+// 9 = 192x256 (8 wavefronts of 96x64), 10 = 128x128 (4 of 64x64), 11 = 64x64 (1), 12 = 128x384
+// (8 of 64x96). DMA kernel: 0 = 256x256 (8 of
 // 128x64, 2 stages), 1 = 256x128 (4 of 128x64, 3 stages), 2 = 128x128 (4 of 64x64, 4 stages),
 // 3 = 128x128 (4 of 64x64, 2 stages, two blocks per CU), 4 = 256x256 (4 of 128x128); persistent
 // 5/6/7. KH_GEMM_TILE forces one (tuning runs).
@@ -872,12 +880,21 @@ int pick_tile(const GemmArgs &g, bool lean) {
   const char *e = getenv("KH_GEMM_TILE");
   const int forced = e ? atoi(e) : -1;
   // (a fused step runs in the lean kernel only)
-  if (forced >= 0 && forced <= 11 && (forced < 8 ? g.epi == EPI_NONE : lean)) return forced;
+  if (forced >= 0 && forced <= 12 && (forced < 8 ? g.epi == EPI_NONE : lean)) return forced;
   // measured on MI355X (f16, random data, encoder shapes M = 13k .. 1.2M): 192x128 leads in
   // general; 192x256 where N is a multiple of 256 and either narrow (N <= 768: one round of tiles
   // at M ~ 13k) or fed by a short K (<= 384, where the epilogue weighs most)
   // (a few hundred rows, e.g. a pooled head: 64 x 64 tiles, enough of them to spread over CUs)
-  if (lean) return g.M <= 1024 ? 11 : g.N % 256 == 0 && (g.N <= 768 || g.K <= 384) ? 9 : 8;
+  if (lean) {
+    if (g.M <= 1024) return 11;
+    const int base = g.N % 256 == 0 && (g.N <= 768 || g.K <= 384) ? 9 : 8;
+    // a row count just past a whole round of 192-row tiles (M = 16384: 86 row tiles) leaves the
+    // last round nearly empty; 128 x 384 tiles divide such shapes into whole rounds
+    const int64_t c_base = base == 9 ? lean_cost(g, 192, 256) : lean_cost(g, 192, 128);
+    // (two blocks of 192 x 128 per CU run about 15 % faster per tile area than 128 x 384)
+    if (g.N % 384 == 0 && lean_cost(g, 128, 384) * 5 < c_base * 4) return 12;
+    return base;
+  }
   if (g.batch == 1 && g.M >= 65536 && g.N >= 1024) return 6;
   return 3;
 }
@@ -897,6 +914,7 @@ void launch_act(const GemmArgs &g, hipStream_t s) {
       case 9: launch_lean<192, 256, 2, 4, ACT>(g, s); return;
       case 10: launch_lean<128, 128, 2, 2, ACT>(g, s); return;
       case 11: launch_lean<64, 64, 1, 1, ACT>(g, s); return;
+      case 12: launch_lean<128, 384, 2, 4, ACT>(g, s); return;
       default: break;
     }
   }
