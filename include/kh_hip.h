@@ -64,6 +64,47 @@ int kh_ctx_weight_bytes(const kh_ctx *ctx, uint64_t *out);
  * reference gathers word rows on the host, src/encoder.ts:271-282); enables kh_upload_ids. */
 int kh_words_set(kh_ctx *ctx, int dtype, int64_t rows, int64_t width, const void *data, size_t bytes);
 
+/* ---- manifest directories (format kleinhirn-weights-2) ------------------------------------ */
+
+#define KH_LOAD_NO_SHA256 1  /* skip the sha256 checks (files verified before) */
+#define KH_LOAD_CHECK_ROWS 2 /* also check every words.bin row against its checksum */
+#define KH_LOAD_NO_WORDS 4   /* leave the word table alone (no device word table) */
+
+typedef struct {
+  int32_t version;       /* manifest version: 3 with words.bin, 2 with keepOnCpu word parts */
+  int32_t tensors;       /* device tensors (keepOnCpu parts excluded) */
+  int32_t shards;
+  int32_t words_dtype;   /* KH_F16 / KH_F32, -1 when no word table was read */
+  int64_t words_rows;
+  int64_t words_width;
+  uint64_t tensor_bytes; /* bytes of the device tensors */
+  uint64_t file_bytes;   /* bytes read: shards and words.bin */
+  double read_ms;        /* manifest parse, file mapping and layout checks */
+  double sha256_ms;      /* hashing, summed over files (they hash in parallel) */
+  double rows_ms;        /* words.bin row checksums (KH_LOAD_CHECK_ROWS) */
+  double upload_ms;      /* host to device copies (kh_load_manifest) */
+} kh_manifest_info;
+
+/* Reads `manifest_path` (manifest.json) and every file it names and applies the checks of the
+ * reference's loader, without a device: shard sizes and sha256 (fetchShardBytes,
+ * src/weights.ts:150-173), words.bin size, row layout and sha256 (fetchWords, src/words.ts:98-114),
+ * or the legacy keepOnCpu word table (loadWords, src/weights.ts:67-90). Errors carry the
+ * reference's messages ("sha256 mismatch on shard-0.bin", ...). */
+int kh_manifest_check(const char *manifest_path, int flags, kh_manifest_info *out);
+
+/* The same checks, then every tensor straight to device memory (as kh_weight_add; replaces
+ * loadWeights' upload loop, src/webgpu-backend.ts:53-101) and the word table as the context's
+ * device word table (as kh_words_set; the row checksums of words.bin stay on the host). Nothing is
+ * uploaded unless every check passes. */
+int kh_load_manifest(kh_ctx *ctx, const char *manifest_path, int flags, kh_manifest_info *out);
+
+/* SHA-256 of `bytes` bytes (the shard digest of src/weights.ts:161-165). */
+int kh_sha256(const void *data, size_t bytes, uint8_t out[32]);
+
+/* Checksum of one words.bin row without its checksum word (rowChecksum, src/words-format.ts:18-32);
+ * `bytes` must be a multiple of 4. */
+int kh_row_checksum(const void *row, size_t bytes, uint32_t row_id, uint32_t salt, uint32_t *out);
+
 /* Backend.check (src/backend.ts:34-35): KH_OK when the plan (JSON of the reference's Plan, typed
  * `init` tables left out) can run here, else an error naming every op that cannot. With a null
  * context only the plan's structure is checked (no weights, no device needed). */

@@ -28,8 +28,12 @@ EXPORTS = [
     "kh_last_error", "kh_abi_version", "kh_ctx_create", "kh_ctx_destroy", "kh_weight_add",
     "kh_ctx_weight_bytes", "kh_words_set", "kh_plan_check", "kh_plan_create", "kh_plan_init_buffer",
     "kh_plan_info_get", "kh_upload", "kh_upload_ids", "kh_run", "kh_read_output", "kh_sync",
-    "kh_last_run_ms", "kh_profile", "kh_packed_rows", "kh_plan_destroy",
+    "kh_last_run_ms", "kh_profile", "kh_packed_rows", "kh_plan_destroy", "kh_manifest_check",
+    "kh_load_manifest", "kh_sha256", "kh_row_checksum",
 ]
+
+# kh_load_manifest / kh_manifest_check flags
+LOAD_NO_SHA256, LOAD_CHECK_ROWS, LOAD_NO_WORDS = 1, 2, 4
 
 
 class KhError(RuntimeError):
@@ -42,6 +46,16 @@ class PlanInfo(ctypes.Structure):
     _fields_ = [("length", ctypes.c_int32), ("batch", ctypes.c_int32), ("markers", ctypes.c_int32),
                 ("f16", ctypes.c_int32), ("bytes", ctypes.c_uint64), ("out_rows", ctypes.c_int32),
                 ("out_cols", ctypes.c_int32), ("launches", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+class ManifestInfo(ctypes.Structure):
+    _fields_ = [("version", ctypes.c_int32), ("tensors", ctypes.c_int32), ("shards", ctypes.c_int32),
+                ("words_dtype", ctypes.c_int32), ("words_rows", ctypes.c_int64), ("words_width", ctypes.c_int64),
+                ("tensor_bytes", ctypes.c_uint64), ("file_bytes", ctypes.c_uint64), ("read_ms", ctypes.c_double),
+                ("sha256_ms", ctypes.c_double), ("rows_ms", ctypes.c_double), ("upload_ms", ctypes.c_double)]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
 
 
 class LaunchStat(ctypes.Structure):
@@ -83,6 +97,10 @@ def lib() -> ctypes.CDLL:
         "kh_profile": [vp, i32, ctypes.POINTER(LaunchStat), i32, ctypes.POINTER(i32)],
         "kh_packed_rows": [vp, ctypes.POINTER(i64)],
         "kh_plan_destroy": [vp],
+        "kh_manifest_check": [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ManifestInfo)],
+        "kh_load_manifest": [vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ManifestInfo)],
+        "kh_sha256": [vp, sz, ctypes.POINTER(ctypes.c_uint8)],
+        "kh_row_checksum": [vp, sz, ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32)],
     }
     for name, args in sigs.items():
         fn = getattr(L, name)
@@ -95,6 +113,30 @@ def lib() -> ctypes.CDLL:
 def _check(rc: int) -> None:
     if rc != 0:
         raise KhError(rc, lib().kh_last_error().decode("utf-8", "replace"))
+
+
+def manifest_check(path: str, flags: int = 0) -> dict:
+    """Reads and checks a manifest directory without a device (kh_manifest_check)."""
+    info = ManifestInfo()
+    _check(lib().kh_manifest_check(os.fsencode(path), flags, ctypes.byref(info)))
+    return info.as_dict()
+
+
+def sha256(data: bytes) -> str:
+    """Hex SHA-256 through the library's implementation (kh_sha256)."""
+    buf = np.frombuffer(bytes(data), dtype=np.uint8)
+    out = (ctypes.c_uint8 * 32)()
+    _check(lib().kh_sha256(buf.ctypes.data if buf.size else None, buf.size, out))
+    return bytes(out).hex()
+
+
+def row_checksum(row: bytes, row_id: int, salt: int) -> int:
+    """words.bin row checksum through the library (kh_row_checksum)."""
+    buf = np.frombuffer(bytes(row), dtype=np.uint8)
+    out = ctypes.c_uint32()
+    _check(lib().kh_row_checksum(buf.ctypes.data if buf.size else None, buf.size, row_id & 0xFFFFFFFF,
+                                 salt & 0xFFFFFFFF, ctypes.byref(out)))
+    return int(out.value)
 
 
 def _ptr(a: np.ndarray | None):
@@ -214,6 +256,17 @@ class HipBackend:
         self.device = device
         for name, t in weights.items():
             self.add_weight(name, t)
+
+    @classmethod
+    def from_manifest(cls, path: str, device: int = 0, flags: int = 0) -> "HipBackend":
+        """A backend whose weights (and device word table) come straight from a manifest directory
+        (kh_load_manifest: loadWeights of src/webgpu-backend.ts:53-101 with the checks of
+        src/weights.ts:150-173). `load_info` holds the sizes and timings of the load."""
+        be = cls({}, device)
+        info = ManifestInfo()
+        _check(lib().kh_load_manifest(be.ctx, os.fsencode(path), flags, ctypes.byref(info)))
+        be.load_info = info.as_dict()
+        return be
 
     def add_weight(self, name: str, t: np.ndarray) -> None:
         t = np.ascontiguousarray(t)

@@ -10,6 +10,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libkh_hip.so")
 SOURCES = ["runner.hip", "gemm.hip", "attention.hip", "rowops.hip"]
+HOST_SOURCES = ["manifest.cpp"]  # host code only: the system C++ compiler
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "-shared", "--offload-arch=gfx950",
@@ -27,6 +28,12 @@ def build(verbose: bool = False) -> str:
         obj = os.path.join(CSRC, "_build", src.replace(".hip", ".o"))
         os.makedirs(os.path.dirname(obj), exist_ok=True)
         cmd = [HIPCC, *[f for f in FLAGS if f != "-shared"], "-c", os.path.join(CSRC, src), "-o", obj]
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+        objs.append(obj)
+    for src in HOST_SOURCES:
+        obj = os.path.join(CSRC, "_build", src.replace(".cpp", ".o"))
+        os.makedirs(os.path.dirname(obj), exist_ok=True)
+        cmd = ["g++", "-O3", "-std=c++17", "-fPIC", "-Wall", "-c", os.path.join(CSRC, src), "-o", obj]
         procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
         objs.append(obj)
     failed = False

@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -27,6 +28,7 @@
 #include "../../include/kh_hip.h"
 #include "json.h"
 #include "kernels.h"
+#include "manifest.h"
 
 namespace kh {
 
@@ -1144,6 +1146,166 @@ int kh_words_set(kh_ctx *ctx, int dtype, int64_t rows, int64_t width, const void
   ctx->words_dtype = dtype;
   ctx->words_rows = rows;
   ctx->words_width = width;
+  KH_API_END
+}
+
+// ---- manifest directories ----------------------------------------------------------------------
+
+// Host-to-device copies from pageable (mapped) memory through two pinned chunks: the CPU fills one
+// chunk while the DMA engine drains the other.
+struct Stager {
+  static constexpr size_t CH = 32u << 20;
+  hipStream_t s = nullptr;
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  HostPinned buf[2];
+  bool pending[2] = {false, false};
+  int cur = 0;
+  size_t used = 0;
+  Stager() {
+    KH_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    KH_CHECK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
+    KH_CHECK(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming));
+    buf[0].ensure(CH);
+    buf[1].ensure(CH);
+  }
+  ~Stager() {
+    if (s) (void)hipStreamSynchronize(s);
+    for (hipEvent_t e : ev)
+      if (e) (void)hipEventDestroy(e);
+    if (s) (void)hipStreamDestroy(s);
+  }
+  void flip() {
+    KH_CHECK(hipEventRecord(ev[cur], s));
+    pending[cur] = true;
+    cur ^= 1;
+    if (pending[cur]) KH_CHECK(hipEventSynchronize(ev[cur]));
+    pending[cur] = false;
+    used = 0;
+  }
+  // `rows` rows of `row` bytes, `stride` bytes apart in host memory, to dst back to back
+  void put_rows(char *dst, const uint8_t *src, size_t rows, size_t row, size_t stride) {
+    while (rows) {
+      if (CH - used < row) flip();
+      const size_t k = std::min(rows, (CH - used) / row);
+      char *b = (char *)buf[cur].p + used;
+      if (stride == row) memcpy(b, src, k * row);
+      else
+        for (size_t i = 0; i < k; i++) memcpy(b + i * row, src + i * stride, row);
+      KH_CHECK(hipMemcpyAsync(dst, b, k * row, hipMemcpyHostToDevice, s));
+      used += k * row;
+      dst += k * row;
+      src += k * stride;
+      rows -= k;
+    }
+  }
+  void put(void *dst, const uint8_t *src, size_t n) {
+    // whole chunks, then the rest
+    const size_t full = n / CH;
+    if (full) put_rows((char *)dst, src, full, CH, CH);
+    if (n % CH) put_rows((char *)dst + full * CH, src + full * CH, 1, n % CH, n % CH);
+  }
+  void finish() { KH_CHECK(hipStreamSynchronize(s)); }
+};
+
+static std::unique_ptr<mf::Loaded> read_manifest(const char *path, int flags) {
+  if (!path || !*path) fail(KH_EINVAL, "null manifest path");
+  try {
+    return mf::load(path, flags);
+  } catch (const std::runtime_error &e) {
+    fail(KH_EINVAL, e.what());
+  }
+  return nullptr;
+}
+
+static void manifest_info(const mf::Loaded &L, kh_manifest_info *out) {
+  memset(out, 0, sizeof(*out));
+  out->version = L.version;
+  out->shards = (int32_t)L.shards.size();
+  out->words_dtype = L.words_dtype;
+  out->words_rows = L.words_rows;
+  out->words_width = L.words_width;
+  for (const mf::Tensor &t : L.tensors)
+    if (!t.keep_on_cpu) {
+      out->tensors++;
+      out->tensor_bytes += t.bytes;
+    }
+  out->file_bytes = L.file_bytes;
+  out->read_ms = L.read_ms;
+  out->sha256_ms = L.sha256_ms;
+  out->rows_ms = L.rows_ms;
+}
+
+int kh_manifest_check(const char *manifest_path, int flags, kh_manifest_info *out) {
+  KH_API_BEGIN
+  auto L = read_manifest(manifest_path, flags);
+  if (out) manifest_info(*L, out);
+  KH_API_END
+}
+
+int kh_load_manifest(kh_ctx *ctx, const char *manifest_path, int flags, kh_manifest_info *out) {
+  KH_API_BEGIN
+  require_live(ctx);
+  auto L = read_manifest(manifest_path, flags);
+  for (const mf::Tensor &t : L->tensors)
+    if (!t.keep_on_cpu && ctx->weights.count(t.name)) fail(KH_EINVAL, "weight " + t.name + " loaded twice");
+  const auto t0 = std::chrono::steady_clock::now();
+  std::vector<std::pair<std::string, uint64_t>> added;
+  try {
+    Stager st;
+    for (const mf::Tensor &t : L->tensors) {
+      if (t.keep_on_cpu) continue;
+      Weight w;
+      w.dtype = t.dtype;
+      w.shape = t.shape;
+      w.count = (int64_t)(t.bytes / elem_size(t.dtype));
+      w.mem.reset(new DevMem());
+      w.mem->alloc(t.bytes);
+      if (t.bytes) st.put(w.mem->p, L->shards[t.shard]->p + t.offset, t.bytes);
+      ctx->weight_bytes += t.bytes;
+      ctx->weights.emplace(t.name, std::move(w));
+      added.push_back({t.name, t.bytes});
+    }
+    std::unique_ptr<DevMem> words;
+    if (L->words_data && !(flags & KH_LOAD_NO_WORDS)) {
+      // rows of words.bin carry a checksum word after the values: the staging copy drops it
+      const size_t row = (size_t)L->words_width * elem_size(L->words_dtype);
+      words.reset(new DevMem());
+      words->alloc(row * (size_t)L->words_rows);
+      st.put_rows((char *)words->p, L->words_data, (size_t)L->words_rows, row, (size_t)L->words_stride);
+    }
+    st.finish();
+    if (words) {
+      ctx->words = std::move(words);
+      ctx->words_dtype = L->words_dtype;
+      ctx->words_rows = L->words_rows;
+      ctx->words_width = L->words_width;
+    }
+  } catch (...) {
+    for (const auto &n : added) {
+      ctx->weight_bytes -= n.second;
+      ctx->weights.erase(n.first);
+    }
+    throw;
+  }
+  if (out) {
+    manifest_info(*L, out);
+    out->upload_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  }
+  KH_API_END
+}
+
+int kh_sha256(const void *data, size_t bytes, uint8_t out[32]) {
+  KH_API_BEGIN
+  if (!out || (bytes && !data)) fail(KH_EINVAL, "null argument");
+  mf::sha256(data, bytes, out);
+  KH_API_END
+}
+
+int kh_row_checksum(const void *row, size_t bytes, uint32_t row_id, uint32_t salt, uint32_t *out) {
+  KH_API_BEGIN
+  if (!out || (bytes && !row)) fail(KH_EINVAL, "null argument");
+  if (bytes % 4) fail(KH_EINVAL, "words: row of " + std::to_string(bytes) + " bytes is not whole u32 words");
+  *out = mf::row_checksum((const uint8_t *)row, bytes, row_id, salt);
   KH_API_END
 }
 

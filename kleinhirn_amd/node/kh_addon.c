@@ -426,6 +426,64 @@ static napi_value last_run_ms(napi_env env, napi_callback_info info) {
   return v;
 }
 
+static napi_value manifest_info_object(napi_env env, const kh_manifest_info *mi) {
+  napi_value o, v;
+  napi_create_object(env, &o);
+#define SET(name, val)                        \
+  napi_create_double(env, (double)(val), &v); \
+  napi_set_named_property(env, o, name, v);
+  SET("version", mi->version);
+  SET("tensors", mi->tensors);
+  SET("shards", mi->shards);
+  SET("wordsDtype", mi->words_dtype);
+  SET("wordsRows", mi->words_rows);
+  SET("wordsWidth", mi->words_width);
+  SET("tensorBytes", mi->tensor_bytes);
+  SET("fileBytes", mi->file_bytes);
+  SET("readMs", mi->read_ms);
+  SET("sha256Ms", mi->sha256_ms);
+  SET("rowsMs", mi->rows_ms);
+  SET("uploadMs", mi->upload_ms);
+#undef SET
+  return o;
+}
+
+/* manifestCheck(path: string, flags?: number) -> info (no device) */
+static napi_value manifest_check(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return NULL;
+  int32_t flags = 0;
+  napi_valuetype t;
+  napi_typeof(env, argv[1], &t);
+  if (t == napi_number) napi_get_value_int32(env, argv[1], &flags);
+  char *path = get_string(env, argv[0], NULL);
+  if (!path) return NULL;
+  kh_manifest_info mi;
+  int rc = kh_manifest_check(path, flags, &mi);
+  free(path);
+  if (rc) return throw_kh(env, rc);
+  return manifest_info_object(env, &mi);
+}
+
+/* loadManifest(ctx, path: string, flags?: number) -> info */
+static napi_value load_manifest(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!get_args(env, info, 3, argv)) return NULL;
+  handle *h = unwrap(env, argv[0], 1);
+  if (!h) return NULL;
+  int32_t flags = 0;
+  napi_valuetype t;
+  napi_typeof(env, argv[2], &t);
+  if (t == napi_number) napi_get_value_int32(env, argv[2], &flags);
+  char *path = get_string(env, argv[1], NULL);
+  if (!path) return NULL;
+  kh_manifest_info mi;
+  int rc = kh_load_manifest((kh_ctx *)h->ptr, path, flags, &mi);
+  free(path);
+  if (rc) return throw_kh(env, rc);
+  return manifest_info_object(env, &mi);
+}
+
 static napi_value abi_version(napi_env env, napi_callback_info info) {
   (void)info;
   napi_value v;
@@ -452,6 +510,8 @@ static napi_value init(napi_env env, napi_value exports) {
       {"readOutput", 0, read_output, 0, 0, 0, napi_default, 0},
       {"readOutputAsync", 0, read_output_async, 0, 0, 0, napi_default, 0},
       {"lastRunMs", 0, last_run_ms, 0, 0, 0, napi_default, 0},
+      {"manifestCheck", 0, manifest_check, 0, 0, 0, napi_default, 0},
+      {"loadManifest", 0, load_manifest, 0, 0, 0, napi_default, 0},
   };
   napi_define_properties(env, exports, sizeof props / sizeof props[0], props);
   return exports;

@@ -14,23 +14,28 @@ const typed = (buf, Ctor) => new Ctor(buf.buffer, buf.byteOffset, buf.byteLength
 
 if (meta.checkOnly) {
   addon.planCheck(null, planText);
-  console.log(JSON.stringify({ ok: true }));
+  // a manifest directory, read and checked without a device
+  const manifest = meta.manifest ? addon.manifestCheck(meta.manifest, meta.manifestFlags || 0) : undefined;
+  console.log(JSON.stringify({ ok: true, manifest }));
   process.exit(0);
 }
 
 (async () => {
   const ctx = addon.ctxCreate(0);
+  // weights from a manifest directory straight to the device, or one tensor at a time
+  const manifest = meta.manifest ? addon.loadManifest(ctx, meta.manifest, meta.manifestFlags || 0) : undefined;
   for (const w of meta.weights) addon.weightAdd(ctx, w.name, w.dtype, w.shape, read(w.file));
   addon.planCheck(ctx, planText);
   const plan = addon.planCreate(ctx, planText);
   for (const [id, file] of Object.entries(meta.inits)) addon.planInitBuffer(plan, id, read(file));
-  const emb = read('emb.bin');
   const tt = meta.typeIds ? typed(read('tt.bin'), Uint32Array) : null;
-  addon.upload(plan, emb, typed(read('mask.bin'), Float32Array), tt);
+  const mask = typed(read('mask.bin'), Float32Array);
+  if (meta.ids) addon.uploadIds(plan, typed(read('ids.bin'), Int32Array), mask, tt);
+  else addon.upload(plan, read('emb.bin'), mask, tt);
   addon.run(plan, meta.rows);
   const out = await addon.readOutputAsync(plan);
   fs.writeFileSync(path.join(dir, 'out.bin'), Buffer.from(out.buffer, out.byteOffset, out.byteLength));
-  console.log(JSON.stringify({ ok: true, n: out.length, ms: addon.lastRunMs(plan), info: addon.planInfo(plan) }));
+  console.log(JSON.stringify({ ok: true, n: out.length, ms: addon.lastRunMs(plan), info: addon.planInfo(plan), manifest }));
   addon.planDestroy(plan);
   addon.ctxDestroy(ctx);
 })().catch((e) => {

@@ -16,14 +16,20 @@ RUNNER = os.path.join(HERE, "node", "run_plan.js")
 
 
 def export_case(dirname: str, plan: dict, weights: dict | None = None, run_input: dict | None = None,
-                rows: int | None = None, check_only: bool = False) -> None:
+                rows: int | None = None, check_only: bool = False, manifest: str | None = None,
+                manifest_flags: int = 0, ids: "np.ndarray | None" = None) -> None:
+    """Case files for run_plan.js. `manifest`: weights from that manifest.json (kh_load_manifest,
+    or kh_manifest_check with check_only); `ids`: token ids for the device word gather."""
     os.makedirs(dirname, exist_ok=True)
     with open(os.path.join(dirname, "plan.json"), "w") as f:
         json.dump(plan_json(plan), f)
     meta = {"checkOnly": check_only, "weights": [], "inits": {}, "rows": rows or 0,
-            "typeIds": bool(run_input is not None and run_input.get("typeIds") is not None)}
+            "typeIds": bool(run_input is not None and run_input.get("typeIds") is not None),
+            "manifest": manifest, "manifestFlags": manifest_flags, "ids": ids is not None}
+    if ids is not None:
+        np.ascontiguousarray(ids, dtype=np.int32).tofile(os.path.join(dirname, "ids.bin"))
     if not check_only:
-        for i, (name, t) in enumerate(weights.items()):
+        for i, (name, t) in enumerate((weights or {}).items()):
             t = np.ascontiguousarray(t)
             fn = f"w{i}.bin"
             t.tofile(os.path.join(dirname, fn))
@@ -34,7 +40,8 @@ def export_case(dirname: str, plan: dict, weights: dict | None = None, run_input
             with open(os.path.join(dirname, fn), "wb") as f:
                 f.write(raw)
             meta["inits"][bid] = fn
-        np.ascontiguousarray(run_input["embeddings"]).tofile(os.path.join(dirname, "emb.bin"))
+        if ids is None:
+            np.ascontiguousarray(run_input["embeddings"]).tofile(os.path.join(dirname, "emb.bin"))
         np.ascontiguousarray(run_input["mask"], dtype=np.float32).tofile(os.path.join(dirname, "mask.bin"))
         if meta["typeIds"]:
             np.ascontiguousarray(run_input["typeIds"], dtype=np.uint32).tofile(os.path.join(dirname, "tt.bin"))

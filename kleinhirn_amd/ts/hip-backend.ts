@@ -14,8 +14,10 @@ import { createRequire } from 'node:module';
 import type { Backend, LoadedBackend, PlanRunner } from './backend.ts';
 import type { RunInput } from './plan/executor.ts';
 import type { Plan } from './plan/ir.ts';
+import { readFileSync } from 'node:fs';
+import { dirname, join } from 'node:path';
 import { fetchShardBytes, loadWords, type Manifest } from './weights.ts';
-import type { WordsFetch } from './words.ts';
+import { legacyTable, wordsView, type WordsFetch, type WordTable } from './words.ts';
 
 // The addon's surface (kleinhirn_amd/node/kh_addon.c); handles are opaque.
 export type KhHandle = { readonly __kh: unique symbol };
@@ -38,7 +40,21 @@ export interface KhAddon {
   readOutput(plan: KhHandle): Float32Array;
   readOutputAsync(plan: KhHandle): Promise<Float32Array>;
   lastRunMs(plan: KhHandle): number;
+  manifestCheck(path: string, flags?: number): ManifestInfo;
+  loadManifest(ctx: KhHandle, path: string, flags?: number): ManifestInfo;
 }
+
+// kh_manifest_info (include/kh_hip.h)
+export interface ManifestInfo {
+  version: number; tensors: number; shards: number; wordsDtype: number; wordsRows: number;
+  wordsWidth: number; tensorBytes: number; fileBytes: number; readMs: number; sha256Ms: number;
+  rowsMs: number; uploadMs: number;
+}
+
+// kh_load_manifest flags
+export const LOAD_NO_SHA256 = 1;
+export const LOAD_CHECK_ROWS = 2;
+export const LOAD_NO_WORDS = 4;
 
 const KH_F32 = 0;
 const KH_F16 = 1;
@@ -142,6 +158,12 @@ export class HipBackend implements Backend {
     this.kh.weightAdd(this.context(), name, dtype === 'f16' ? KH_F16 : KH_F32, shape, bytes);
   }
 
+  // Every tensor of a manifest directory on the local disk, checked and copied to device memory by
+  // the library (kh_load_manifest), and its word table as the device word table.
+  loadManifest(path: string, flags = 0): ManifestInfo {
+    return this.kh.loadManifest(this.context(), path, flags);
+  }
+
   // Device-resident word table: runs by token id gather rows on the GPU (kh_upload_ids).
   setWords(dtype: 'f16' | 'f32', rows: number, width: number, bytes: Uint8Array): void {
     this.kh.wordsSet(this.context(), dtype === 'f16' ? KH_F16 : KH_F32, rows, width, bytes);
@@ -210,5 +232,46 @@ export async function loadHip(
     backend, words: words.table, downloadBytes: fetched.downloadBytes + words.bytes,
     timing: { fetchMs: fetched.fetchMs, bodyMs: fetched.bodyMs, sha256Ms: fetched.sha256Ms, uploadMs,
       ...words.timing },
+  };
+}
+
+// A manifest directory on the local disk: the library maps the files, applies the checks of
+// fetchShardBytes / fetchWords (src/weights.ts:150-173, src/words.ts:98-114) and copies every
+// tensor and the word table to device memory with no JS-side copy. The host keeps its WordTable
+// view of the same word rows for the reference's host gather (src/encoder.ts:273-282).
+export function loadHipLocal(
+  manifestPath: string, options: { device?: number; addon?: KhAddon; flags?: number } = {},
+): LoadedBackend & { manifest: Manifest; info: ManifestInfo } {
+  const kh = options.addon ?? loadAddon();
+  const manifest = JSON.parse(readFileSync(manifestPath, 'utf8')) as Manifest;
+  const backend = new HipBackend(kh, options.device ?? 0);
+  let info: ManifestInfo;
+  try {
+    info = backend.loadManifest(manifestPath, options.flags ?? 0);
+  } catch (e) {
+    backend.dispose();
+    throw e;
+  }
+  const base = dirname(manifestPath);
+  const bytesOf = (b: Buffer): ArrayBuffer => b.buffer.slice(b.byteOffset, b.byteOffset + b.byteLength) as ArrayBuffer;
+  let words: WordTable;
+  if (manifest.words) {
+    words = wordsView(bytesOf(readFileSync(join(base, manifest.words.file))), manifest.words);
+  } else {
+    // legacy: the keepOnCpu parts in row order (loadWords, src/weights.ts:67-90)
+    const parts = manifest.tensors.filter((t) => t.keepOnCpu).sort((a, b) => (a.rowStart ?? 0) - (b.rowStart ?? 0));
+    const joined = new Uint8Array(parts.reduce((n, t) => n + t.byteLength, 0));
+    let at = 0;
+    for (const t of parts) {
+      const shard = readFileSync(join(base, manifest.shards[t.shard].file));
+      joined.set(shard.subarray(t.offset, t.offset + t.byteLength), at);
+      at += t.byteLength;
+    }
+    words = legacyTable(joined.buffer, parts[0].dtype === 'f16' ? 'f16' : 'f32', parts[0].shape[1]);
+  }
+  return {
+    backend, words, manifest, info, downloadBytes: info.fileBytes,
+    timing: { fetchMs: info.readMs, bodyMs: 0, sha256Ms: info.sha256Ms, uploadMs: info.uploadMs,
+      embedJoinMs: 0, wordsFetchMs: 0, wordsSha256Ms: 0 },
   };
 }

@@ -53,3 +53,46 @@ def test_node_path_matches_python_path_and_golden():
     assert np.array_equal(got, py)
     d = decision_parity(ref, got)
     assert d["mismatched"] == 0, d
+
+
+def test_node_addon_checks_a_manifest_directory():
+    """manifestCheck through the addon reads what kh_manifest_check reads."""
+    from kleinhirn_amd import backend as B
+    from oracle import manifest_format as MF
+    w = configs.c2()
+    rng = np.random.default_rng(1)
+    weights = {MF.WORDS: rng.standard_normal((50, 16)).astype(np.float32),
+               "x.weight": rng.standard_normal((8, 16)).astype(np.float32)}
+    with tempfile.TemporaryDirectory() as d:
+        path = MF.write_manifest(os.path.join(d, "m"), weights, "f16")
+        export_case(d, build_plan(w.spec, w.head, 64, 1, True), check_only=True, manifest=path,
+                    manifest_flags=B.LOAD_CHECK_ROWS)
+        res = run_node(d)
+        want = B.manifest_check(path, B.LOAD_CHECK_ROWS)
+    got = res["manifest"]
+    assert (got["version"], got["tensors"], got["wordsRows"], got["wordsWidth"]) == (
+        want["version"], want["tensors"], want["words_rows"], want["words_width"]) == (3, 1, 50, 16)
+    assert got["fileBytes"] == want["file_bytes"]
+
+
+@pytest.mark.gpu
+def test_node_manifest_load_and_device_gather_match_python_path():
+    """loadManifest + uploadIds through the addon (weights and word table from the files, rows
+    gathered on the device) against the Python host's tensor-by-tensor upload and host gather."""
+    from oracle import manifest_format as MF
+    from tests.helpers import hip_outputs
+    from tests.test_gpu_models import case_and_oracle
+    case, _ = case_and_oracle("c2")
+    plan = build_plan(case.spec, case.head, case.length, len(case.ids), True)
+    mask, tt = inputs.mask_and_types(case.spec, case.ids, case.length)
+    ids = np.zeros(case.length * len(case.ids), dtype=np.int32)
+    for b, seq in enumerate(case.ids):
+        ids[b * case.length:b * case.length + len(seq)] = seq
+    with tempfile.TemporaryDirectory() as d:
+        path = MF.write_manifest(os.path.join(d, "m"), case.weights, "f16")
+        export_case(d, plan, {}, {"embeddings": None, "mask": mask, "typeIds": tt},
+                    rows=case.length * len(case.ids), manifest=path, ids=ids)
+        res = run_node(d)
+        got = np.fromfile(os.path.join(d, "out.bin"), dtype=np.float32).reshape(len(case.ids), -1)
+    assert res["ok"] and res["manifest"]["tensors"] > 0
+    assert np.array_equal(got, hip_outputs(case, f16=True))

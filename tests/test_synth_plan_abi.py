@@ -151,7 +151,7 @@ def test_validate_segments_rejects_double_bound_writable_buffer():
 
 def header_symbols():
     text = open(os.path.join(ROOT, "include", "kh_hip.h")).read()
-    return sorted(set(re.findall(r"\b(kh_[a-z_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(kh_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol():
