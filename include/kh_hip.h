@@ -105,6 +105,28 @@ int kh_sha256(const void *data, size_t bytes, uint8_t out[32]);
  * `bytes` must be a multiple of 4. */
 int kh_row_checksum(const void *row, size_t bytes, uint32_t row_id, uint32_t salt, uint32_t *out);
 
+/* ---- scores from the outputs (the step after the plan) ------------------------------------ */
+
+#define KH_SCORES_SOFTMAX 0 /* single-label classification: softmax per row, label = its argmax */
+#define KH_SCORES_SIGMOID 1 /* multi-label: 1 / (1 + e^-logit), label = argmax of the logits */
+#define KH_SCORES_RAW 2     /* regression: the logits, label = their argmax */
+#define KH_SCORES_L2 3      /* embeddings: rows divided by max(|row|, 1e-12) */
+
+/* Scores of a row-major [rows, cols] f32 array in the reference's arithmetic (f32 values,
+ * double operations, one rounding to f32; softmax, l2normalize, argmaxRows with ties to the
+ * lower index, src/tasks.ts:22-42, 72-84; the per-problem choice of classify,
+ * src/encoder.ts:498-513). `index` (one per row) may be null. A non-finite input fails with
+ * "output: k of n values are not finite" (assertFinite, src/tasks.ts:5-9). */
+int kh_scores(const float *logits, int64_t rows, int32_t cols, int kind, float *scores, int32_t *index);
+
+/* kh_read_output followed by kh_scores on the plan's output (pooled heads: one row per
+ * sequence). */
+int kh_read_scores(kh_plan *plan, int kind, float *scores, size_t count, int32_t *index, size_t index_count);
+
+/* Indices of `n` scores by score, highest first, equal scores in index order (rerank,
+ * src/encoder.ts:533-544). */
+int kh_rank(const float *scores, int64_t n, int32_t *order);
+
 /* Backend.check (src/backend.ts:34-35): KH_OK when the plan (JSON of the reference's Plan, typed
  * `init` tables left out) can run here, else an error naming every op that cannot. With a null
  * context only the plan's structure is checked (no weights, no device needed). */

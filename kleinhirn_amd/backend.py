@@ -29,8 +29,11 @@ EXPORTS = [
     "kh_ctx_weight_bytes", "kh_words_set", "kh_plan_check", "kh_plan_create", "kh_plan_init_buffer",
     "kh_plan_info_get", "kh_upload", "kh_upload_ids", "kh_run", "kh_read_output", "kh_sync",
     "kh_last_run_ms", "kh_profile", "kh_packed_rows", "kh_plan_destroy", "kh_manifest_check",
-    "kh_load_manifest", "kh_sha256", "kh_row_checksum",
+    "kh_load_manifest", "kh_sha256", "kh_row_checksum", "kh_scores", "kh_read_scores", "kh_rank",
 ]
+
+# kh_scores kinds
+SCORES_SOFTMAX, SCORES_SIGMOID, SCORES_RAW, SCORES_L2 = 0, 1, 2, 3
 
 # kh_load_manifest / kh_manifest_check flags
 LOAD_NO_SHA256, LOAD_CHECK_ROWS, LOAD_NO_WORDS = 1, 2, 4
@@ -101,6 +104,9 @@ def lib() -> ctypes.CDLL:
         "kh_load_manifest": [vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ManifestInfo)],
         "kh_sha256": [vp, sz, ctypes.POINTER(ctypes.c_uint8)],
         "kh_row_checksum": [vp, sz, ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32)],
+        "kh_scores": [vp, i64, i32, ctypes.c_int, vp, vp],
+        "kh_read_scores": [vp, ctypes.c_int, vp, sz, vp, sz],
+        "kh_rank": [vp, i64, vp],
     }
     for name, args in sigs.items():
         fn = getattr(L, name)
@@ -137,6 +143,25 @@ def row_checksum(row: bytes, row_id: int, salt: int) -> int:
     _check(lib().kh_row_checksum(buf.ctypes.data if buf.size else None, buf.size, row_id & 0xFFFFFFFF,
                                  salt & 0xFFFFFFFF, ctypes.byref(out)))
     return int(out.value)
+
+
+def scores(logits: np.ndarray, kind: int = SCORES_SOFTMAX) -> tuple[np.ndarray, np.ndarray]:
+    """Scores and label index per row of a [rows, cols] f32 array (kh_scores)."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    if x.ndim == 1:
+        x = x[None]
+    out = np.empty_like(x)
+    idx = np.empty(x.shape[0], dtype=np.int32)
+    _check(lib().kh_scores(x.ctypes.data, x.shape[0], x.shape[1], kind, out.ctypes.data, idx.ctypes.data))
+    return out, idx
+
+
+def rank(values: np.ndarray) -> np.ndarray:
+    """Indices by score, highest first, ties in index order (kh_rank)."""
+    x = np.ascontiguousarray(values, dtype=np.float32).ravel()
+    order = np.empty(x.size, dtype=np.int32)
+    _check(lib().kh_rank(x.ctypes.data if x.size else None, x.size, order.ctypes.data if x.size else None))
+    return order
 
 
 def _ptr(a: np.ndarray | None):
@@ -207,6 +232,14 @@ class HipPlanRunner:
         out = np.empty(o["rows"] * o["cols"], dtype=np.float32)
         _check(lib().kh_read_output(self.h, _ptr(out), out.size))
         return out
+
+    def read_scores(self, kind: int = SCORES_SOFTMAX) -> tuple[np.ndarray, np.ndarray]:
+        """The output's scores and label per row (kh_read_scores; pooled heads)."""
+        o = self.plan["output"]
+        out = np.empty((o["rows"], o["cols"]), dtype=np.float32)
+        idx = np.empty(o["rows"], dtype=np.int32)
+        _check(lib().kh_read_scores(self.h, kind, out.ctypes.data, out.size, idx.ctypes.data, idx.size))
+        return out, idx
 
     def read_capture(self):
         raise RuntimeError("capture is a WebGPU parity tool; the HIP runner has no capture")

@@ -29,6 +29,7 @@
 #include "json.h"
 #include "kernels.h"
 #include "manifest.h"
+#include "postprocess.h"
 
 namespace kh {
 
@@ -1653,6 +1654,46 @@ int kh_read_output(kh_plan *plan, float *out, size_t count) {
     latch(plan->ctx, e);
     throw;
   }
+  KH_API_END
+}
+
+static void scores_of(const float *logits, int64_t rows, int32_t cols, int kind, float *scores, int32_t *index) {
+  if (kind < KH_SCORES_SOFTMAX || kind > KH_SCORES_L2) fail(KH_EINVAL, "scores kind " + std::to_string(kind));
+  if (rows < 0 || cols <= 0) fail(KH_EINVAL, "scores of " + std::to_string(rows) + " x " + std::to_string(cols));
+  if (rows && (!logits || !scores)) fail(KH_EINVAL, "null argument");
+  const int64_t bad = post::count_nonfinite(logits, rows * cols);
+  if (bad)
+    fail(KH_EINVAL, "output: " + std::to_string(bad) + " of " + std::to_string(rows * cols) + " values are not finite");
+  for (int64_t r = 0; r < rows; r++)
+    post::row_scores(logits + r * cols, cols, kind, scores + r * cols, index ? index + r : nullptr);
+}
+
+int kh_scores(const float *logits, int64_t rows, int32_t cols, int kind, float *scores, int32_t *index) {
+  KH_API_BEGIN
+  scores_of(logits, rows, cols, kind, scores, index);
+  KH_API_END
+}
+
+int kh_read_scores(kh_plan *plan, int kind, float *scores, size_t count, int32_t *index, size_t index_count) {
+  KH_API_BEGIN
+  if (!plan || !scores) fail(KH_EINVAL, "null argument");
+  if (plan->out_packed) fail(KH_EUNSUPPORTED, "scores of token rows: read the output and call kh_scores");
+  const size_t n = (size_t)plan->out_rows * plan->out_cols;
+  if (count < n) fail(KH_EINVAL, "output holds " + std::to_string(n) + " values, the array " + std::to_string(count));
+  if (index && index_count < (size_t)plan->out_rows) fail(KH_EINVAL, "index array shorter than the output rows");
+  std::vector<float> raw(n);
+  const int rc = kh_read_output(plan, raw.data(), n);
+  if (rc) fail(rc, kh_last_error());
+  scores_of(raw.data(), plan->out_rows, plan->out_cols, kind, scores, index);
+  KH_API_END
+}
+
+int kh_rank(const float *scores, int64_t n, int32_t *order) {
+  KH_API_BEGIN
+  if (n < 0 || (n && (!scores || !order))) fail(KH_EINVAL, "null argument");
+  const int64_t bad = post::count_nonfinite(scores, n);
+  if (bad) fail(KH_EINVAL, "output: " + std::to_string(bad) + " of " + std::to_string(n) + " values are not finite");
+  post::rank(scores, n, order);
   KH_API_END
 }
 

@@ -484,6 +484,58 @@ static napi_value load_manifest(napi_env env, napi_callback_info info) {
   return manifest_info_object(env, &mi);
 }
 
+/* scores(logits: Float32Array, cols: number, kind: number) -> { scores: Float32Array, index: Int32Array } */
+static napi_value scores(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!get_args(env, info, 3, argv)) return NULL;
+  void *data;
+  size_t bytes;
+  if (!get_bytes(env, argv[0], &data, &bytes)) {
+    napi_throw_type_error(env, NULL, "logits must be a Float32Array");
+    return NULL;
+  }
+  int32_t cols = 0, kind = 0;
+  napi_get_value_int32(env, argv[1], &cols);
+  napi_get_value_int32(env, argv[2], &kind);
+  if (cols <= 0) {
+    napi_throw_range_error(env, NULL, "cols must be positive");
+    return NULL;
+  }
+  const size_t n = bytes / 4, rows = n / (size_t)cols;
+  napi_value sab, iab, sarr, iarr, o;
+  void *sp, *ip;
+  CHECK_NAPI(env, napi_create_arraybuffer(env, n * 4, &sp, &sab));
+  CHECK_NAPI(env, napi_create_arraybuffer(env, rows * 4 + 4, &ip, &iab));
+  int rc = kh_scores((const float *)data, (int64_t)rows, cols, kind, (float *)sp, (int32_t *)ip);
+  if (rc) return throw_kh(env, rc);
+  CHECK_NAPI(env, napi_create_typedarray(env, napi_float32_array, n, sab, 0, &sarr));
+  CHECK_NAPI(env, napi_create_typedarray(env, napi_int32_array, rows, iab, 0, &iarr));
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "scores", sarr);
+  napi_set_named_property(env, o, "index", iarr);
+  return o;
+}
+
+/* rank(scores: Float32Array) -> Int32Array (highest first, ties in index order) */
+static napi_value rank(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  void *data;
+  size_t bytes;
+  if (!get_bytes(env, argv[0], &data, &bytes)) {
+    napi_throw_type_error(env, NULL, "scores must be a Float32Array");
+    return NULL;
+  }
+  const size_t n = bytes / 4;
+  napi_value ab, arr;
+  void *op;
+  CHECK_NAPI(env, napi_create_arraybuffer(env, n * 4 + 4, &op, &ab));
+  int rc = kh_rank((const float *)data, (int64_t)n, (int32_t *)op);
+  if (rc) return throw_kh(env, rc);
+  CHECK_NAPI(env, napi_create_typedarray(env, napi_int32_array, n, ab, 0, &arr));
+  return arr;
+}
+
 static napi_value abi_version(napi_env env, napi_callback_info info) {
   (void)info;
   napi_value v;
@@ -512,6 +564,8 @@ static napi_value init(napi_env env, napi_value exports) {
       {"lastRunMs", 0, last_run_ms, 0, 0, 0, napi_default, 0},
       {"manifestCheck", 0, manifest_check, 0, 0, 0, napi_default, 0},
       {"loadManifest", 0, load_manifest, 0, 0, 0, napi_default, 0},
+      {"scores", 0, scores, 0, 0, 0, napi_default, 0},
+      {"rank", 0, rank, 0, 0, 0, napi_default, 0},
   };
   napi_define_properties(env, exports, sizeof props / sizeof props[0], props);
   return exports;

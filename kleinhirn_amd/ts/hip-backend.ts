@@ -42,7 +42,16 @@ export interface KhAddon {
   lastRunMs(plan: KhHandle): number;
   manifestCheck(path: string, flags?: number): ManifestInfo;
   loadManifest(ctx: KhHandle, path: string, flags?: number): ManifestInfo;
+  // kh_scores / kh_rank: the numeric steps after the plan (src/tasks.ts, src/encoder.ts:498-544)
+  scores(logits: Float32Array, cols: number, kind: number): { scores: Float32Array; index: Int32Array };
+  rank(scores: Float32Array): Int32Array;
 }
+
+// kh_scores kinds: single-label softmax, multi-label sigmoid, regression, L2-normalised embedding
+export const SCORES_SOFTMAX = 0;
+export const SCORES_SIGMOID = 1;
+export const SCORES_RAW = 2;
+export const SCORES_L2 = 3;
 
 // kh_manifest_info (include/kh_hip.h)
 export interface ManifestInfo {

@@ -172,3 +172,31 @@ def test_cls_tail_with_empty_sequences_and_moved_markers(monkeypatch):
     assert np.array_equal(pruned_moved, full_moved)
     assert not np.array_equal(pruned_moved[1], pruned[1])
     assert np.array_equal(np.delete(pruned_moved, 1, axis=0), np.delete(pruned, 1, axis=0))
+
+
+@pytest.mark.parametrize("key", ["c2", "c5", "c4"])
+def test_read_scores_equals_scores_of_the_output(key):
+    """kh_read_scores on the device output equals kh_scores of kh_read_output, and its labels
+    equal the oracle's decisions wherever f16 rounding cannot flip them."""
+    from kleinhirn_amd import backend as B
+    from oracle import postprocess as P
+    case, ref = case_and_oracle(key)
+    kind = {"c2": B.SCORES_SOFTMAX, "c5": B.SCORES_RAW, "c4": B.SCORES_L2}[key]
+    W = configs.storage(case.weights, True)
+    be = B.HipBackend(W)
+    plan = build_plan(case.spec, case.head, case.length, len(case.ids), True)
+    r = be.runner(plan)
+    r.upload(inputs.run_input(case.spec, W["embeddings.word.weight"], case.ids, case.length))
+    r.run(case.length * len(case.ids))
+    out = r.read_output().reshape(len(case.ids), -1)
+    s, idx = r.read_scores(kind)
+    s2, idx2 = B.scores(out, kind)
+    assert np.array_equal(s, s2) and np.array_equal(idx, idx2)
+    want, widx = P.scores(ref.astype(np.float32), kind)
+    if kind == B.SCORES_SOFTMAX:
+        d = decision_parity(ref, out)
+        assert d["mismatched"] == 0, d
+    if kind == B.SCORES_L2:
+        assert cosine_rows(want, s).min() >= 0.999
+    r.destroy()
+    be.dispose()

@@ -96,3 +96,23 @@ def test_node_manifest_load_and_device_gather_match_python_path():
         got = np.fromfile(os.path.join(d, "out.bin"), dtype=np.float32).reshape(len(case.ids), -1)
     assert res["ok"] and res["manifest"]["tensors"] > 0
     assert np.array_equal(got, hip_outputs(case, f16=True))
+
+
+def test_node_addon_scores_and_rank_equal_the_oracle():
+    import json
+    import subprocess
+    from oracle import postprocess as P
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((9, 3)) * 3).astype(np.float32)
+    code = (f"const a = require({json.dumps(ADDON)});"
+            f"const x = new Float32Array({json.dumps(x.ravel().tolist())});"
+            "const r = a.scores(x, 3, 0);"
+            "console.log(JSON.stringify({s: Array.from(r.scores), i: Array.from(r.index),"
+            " o: Array.from(a.rank(new Float32Array([0.25, 3, 0.25, -2, 3])))}));")
+    out = subprocess.run(["node", "-e", code], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stderr
+    res = json.loads(out.stdout)
+    want, wi = P.scores(x, P.SOFTMAX)
+    assert np.array_equal(np.array(res["s"], np.float32).reshape(9, 3), want)
+    assert res["i"] == wi.tolist()
+    assert res["o"] == [1, 4, 0, 2, 3]
