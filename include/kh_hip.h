@@ -105,6 +105,37 @@ int kh_sha256(const void *data, size_t bytes, uint8_t out[32]);
  * `bytes` must be a multiple of 4. */
 int kh_row_checksum(const void *row, size_t bytes, uint32_t row_id, uint32_t salt, uint32_t *out);
 
+/* ---- batch scheduling over packed plans ----------------------------------------------------- */
+
+typedef struct kh_sched kh_sched;
+
+typedef struct {
+  int32_t chunks;     /* plan runs */
+  int32_t sequences;
+  int64_t tokens;     /* valid rows computed */
+  double wall_ms;     /* kh_sched_run from entry to return */
+  double gpu_ms;      /* summed kh_last_run_ms of the runs */
+  double host_ms;     /* packing, uploads and submits (overlapping the device) */
+} kh_sched_stats;
+
+/* A scheduler over `n` created plans of one context (their init tables set; the context's device
+ * word table set), all pooled heads with the same output columns. The plans stay the caller's and
+ * must outlive the scheduler. Replaces the chunking of runIdsBatch (src/encoder.ts:380-436: chunks
+ * of at most 16 rows on plans of 1/4/8/16 sequences, src/cache.ts:9-18) for packed plans. */
+int kh_sched_create(kh_plan *const *plans, int32_t n, kh_sched **out);
+
+/* Runs `nseq` token id sequences (sequence i is ids[offsets[i] .. offsets[i + 1])) and writes one
+ * output row per sequence, in input order. Sequences go in length order (sortByKey,
+ * src/cache.ts:92-108) into chunks of at most B sequences of the plan with the smallest length
+ * holding them, and at most `token_budget` tokens when it is positive; plans of one shape run in
+ * turn, so the next chunk is packed while the previous one computes. `type_words` (nullable) holds
+ * the u32 type word per token in the layout of `ids` (type in the low 16 bits, the position row of
+ * POSIDS plans in the high 16, as kh_upload). */
+int kh_sched_run(kh_sched *s, const int32_t *ids, const int64_t *offsets, int64_t nseq, const uint32_t *type_words,
+                 int64_t token_budget, float *out, size_t out_count, kh_sched_stats *stats);
+
+int kh_sched_destroy(kh_sched *s);
+
 /* ---- scores from the outputs (the step after the plan) ------------------------------------ */
 
 #define KH_SCORES_SOFTMAX 0 /* single-label classification: softmax per row, label = its argmax */

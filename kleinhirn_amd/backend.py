@@ -30,6 +30,7 @@ EXPORTS = [
     "kh_plan_info_get", "kh_upload", "kh_upload_ids", "kh_run", "kh_read_output", "kh_sync",
     "kh_last_run_ms", "kh_profile", "kh_packed_rows", "kh_plan_destroy", "kh_manifest_check",
     "kh_load_manifest", "kh_sha256", "kh_row_checksum", "kh_scores", "kh_read_scores", "kh_rank",
+    "kh_sched_create", "kh_sched_run", "kh_sched_destroy",
 ]
 
 # kh_scores kinds
@@ -56,6 +57,14 @@ class ManifestInfo(ctypes.Structure):
                 ("words_dtype", ctypes.c_int32), ("words_rows", ctypes.c_int64), ("words_width", ctypes.c_int64),
                 ("tensor_bytes", ctypes.c_uint64), ("file_bytes", ctypes.c_uint64), ("read_ms", ctypes.c_double),
                 ("sha256_ms", ctypes.c_double), ("rows_ms", ctypes.c_double), ("upload_ms", ctypes.c_double)]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+class SchedStats(ctypes.Structure):
+    _fields_ = [("chunks", ctypes.c_int32), ("sequences", ctypes.c_int32), ("tokens", ctypes.c_int64),
+                ("wall_ms", ctypes.c_double), ("gpu_ms", ctypes.c_double), ("host_ms", ctypes.c_double)]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -107,6 +116,9 @@ def lib() -> ctypes.CDLL:
         "kh_scores": [vp, i64, i32, ctypes.c_int, vp, vp],
         "kh_read_scores": [vp, ctypes.c_int, vp, sz, vp, sz],
         "kh_rank": [vp, i64, vp],
+        "kh_sched_create": [ctypes.POINTER(vp), i32, ctypes.POINTER(vp)],
+        "kh_sched_run": [vp, vp, vp, i64, vp, i64, vp, sz, ctypes.POINTER(SchedStats)],
+        "kh_sched_destroy": [vp],
     }
     for name, args in sigs.items():
         fn = getattr(L, name)

@@ -10,7 +10,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libkh_hip.so")
 SOURCES = ["runner.hip", "gemm.hip", "attention.hip", "rowops.hip"]
-HOST_SOURCES = ["manifest.cpp", "postprocess.cpp"]  # host code only: the system C++ compiler
+HOST_SOURCES = ["manifest.cpp", "postprocess.cpp", "sched.cpp"]  # host code only: the system C++ compiler
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "-shared", "--offload-arch=gfx950",

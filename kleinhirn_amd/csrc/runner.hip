@@ -1070,6 +1070,11 @@ static void require_live(kh_ctx *ctx) {
   KH_CHECK(hipSetDevice(ctx->device));
 }
 
+namespace kh {
+// the message kh_last_error() returns, for the host-only parts of the library (sched.cpp)
+void set_last_error(const std::string &m) { g_last_error = m; }
+}  // namespace kh
+
 extern "C" {
 
 const char *kh_last_error(void) { return g_last_error.c_str(); }

@@ -33,7 +33,7 @@ static napi_value throw_kh(napi_env env, int rc) {
 
 typedef struct {
   void *ptr;
-  int kind; /* 1 ctx, 2 plan */
+  int kind; /* 1 ctx, 2 plan, 3 scheduler */
 } handle;
 
 static void finalize_handle(napi_env env, void *data, void *hint) {
@@ -43,6 +43,7 @@ static void finalize_handle(napi_env env, void *data, void *hint) {
   /* explicit destroy() is the contract; a garbage-collected handle frees its native object */
   if (h->ptr) {
     if (h->kind == 2) kh_plan_destroy((kh_plan *)h->ptr);
+    else if (h->kind == 3) kh_sched_destroy((kh_sched *)h->ptr);
     else kh_ctx_destroy((kh_ctx *)h->ptr);
   }
   free(h);
@@ -60,7 +61,9 @@ static napi_value wrap(napi_env env, void *ptr, int kind) {
 static handle *unwrap(napi_env env, napi_value v, int kind) {
   void *data = NULL;
   if (napi_get_value_external(env, v, &data) != napi_ok || !data || ((handle *)data)->kind != kind) {
-    napi_throw_type_error(env, NULL, kind == 2 ? "expected a plan handle" : "expected a context handle");
+    napi_throw_type_error(env, NULL, kind == 2   ? "expected a plan handle"
+                                     : kind == 3 ? "expected a scheduler handle"
+                                                 : "expected a context handle");
     return NULL;
   }
   return (handle *)data;
@@ -134,7 +137,10 @@ static napi_value destroy(napi_env env, napi_callback_info info) {
   }
   handle *h = (handle *)data;
   int rc = 0;
-  if (h->ptr) rc = h->kind == 2 ? kh_plan_destroy((kh_plan *)h->ptr) : kh_ctx_destroy((kh_ctx *)h->ptr);
+  if (h->ptr)
+    rc = h->kind == 2   ? kh_plan_destroy((kh_plan *)h->ptr)
+         : h->kind == 3 ? kh_sched_destroy((kh_sched *)h->ptr)
+                        : kh_ctx_destroy((kh_ctx *)h->ptr);
   h->ptr = NULL;
   if (rc) return throw_kh(env, rc);
   return NULL;
@@ -536,6 +542,80 @@ static napi_value rank(napi_env env, napi_callback_info info) {
   return arr;
 }
 
+/* schedCreate(plans: handle[]) -> scheduler handle (the plans must outlive it) */
+static napi_value sched_create(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  uint32_t n = 0;
+  if (napi_get_array_length(env, argv[0], &n) != napi_ok || n == 0) {
+    napi_throw_type_error(env, NULL, "expected an array of plan handles");
+    return NULL;
+  }
+  kh_plan **plans = (kh_plan **)malloc(n * sizeof(kh_plan *));
+  for (uint32_t i = 0; i < n; i++) {
+    napi_value e;
+    napi_get_element(env, argv[0], i, &e);
+    handle *h = unwrap(env, e, 2);
+    if (!h) {
+      free(plans);
+      return NULL;
+    }
+    plans[i] = (kh_plan *)h->ptr;
+  }
+  kh_sched *s = NULL;
+  int rc = kh_sched_create(plans, (int32_t)n, &s);
+  free(plans);
+  if (rc) return throw_kh(env, rc);
+  return wrap(env, s, 3);
+}
+
+/* schedRun(s, ids: Int32Array, offsets: Float64Array, typeWords: Uint32Array | null, tokenBudget,
+ *          cols) -> { out: Float32Array, stats } */
+static napi_value sched_run(napi_env env, napi_callback_info info) {
+  napi_value argv[6];
+  if (!get_args(env, info, 6, argv)) return NULL;
+  handle *h = unwrap(env, argv[0], 3);
+  if (!h) return NULL;
+  void *ids, *offs, *tw;
+  size_t ids_b, offs_b, tw_b;
+  if (!get_bytes(env, argv[1], &ids, &ids_b) || !get_bytes(env, argv[2], &offs, &offs_b) ||
+      !get_bytes(env, argv[3], &tw, &tw_b) || offs_b < 8) {
+    napi_throw_type_error(env, NULL, "schedRun(s, ids, offsets, typeWords, tokenBudget, cols)");
+    return NULL;
+  }
+  double budget = 0;
+  int32_t cols = 0;
+  napi_get_value_double(env, argv[4], &budget);
+  napi_get_value_int32(env, argv[5], &cols);
+  const size_t nseq = offs_b / 8 - 1;
+  int64_t *o64 = (int64_t *)malloc((nseq + 1) * 8);
+  for (size_t i = 0; i <= nseq; i++) o64[i] = (int64_t)((const double *)offs)[i];
+  napi_value ab, arr, res, st, v;
+  void *op;
+  CHECK_NAPI(env, napi_create_arraybuffer(env, nseq * (size_t)cols * 4 + 4, &op, &ab));
+  kh_sched_stats ss;
+  int rc = kh_sched_run((kh_sched *)h->ptr, (const int32_t *)ids, o64, (int64_t)nseq, (const uint32_t *)tw,
+                        (int64_t)budget, (float *)op, nseq * (size_t)cols, &ss);
+  free(o64);
+  if (rc) return throw_kh(env, rc);
+  CHECK_NAPI(env, napi_create_typedarray(env, napi_float32_array, nseq * (size_t)cols, ab, 0, &arr));
+  napi_create_object(env, &st);
+#define SET(name, val)                        \
+  napi_create_double(env, (double)(val), &v); \
+  napi_set_named_property(env, st, name, v);
+  SET("chunks", ss.chunks);
+  SET("sequences", ss.sequences);
+  SET("tokens", ss.tokens);
+  SET("wallMs", ss.wall_ms);
+  SET("gpuMs", ss.gpu_ms);
+  SET("hostMs", ss.host_ms);
+#undef SET
+  napi_create_object(env, &res);
+  napi_set_named_property(env, res, "out", arr);
+  napi_set_named_property(env, res, "stats", st);
+  return res;
+}
+
 static napi_value abi_version(napi_env env, napi_callback_info info) {
   (void)info;
   napi_value v;
@@ -566,6 +646,9 @@ static napi_value init(napi_env env, napi_value exports) {
       {"loadManifest", 0, load_manifest, 0, 0, 0, napi_default, 0},
       {"scores", 0, scores, 0, 0, 0, napi_default, 0},
       {"rank", 0, rank, 0, 0, 0, napi_default, 0},
+      {"schedCreate", 0, sched_create, 0, 0, 0, napi_default, 0},
+      {"schedRun", 0, sched_run, 0, 0, 0, napi_default, 0},
+      {"schedDestroy", 0, destroy, 0, 0, 0, napi_default, 0},
   };
   napi_define_properties(env, exports, sizeof props / sizeof props[0], props);
   return exports;

@@ -26,6 +26,22 @@ if (meta.checkOnly) {
   const manifest = meta.manifest ? addon.loadManifest(ctx, meta.manifest, meta.manifestFlags || 0) : undefined;
   for (const w of meta.weights) addon.weightAdd(ctx, w.name, w.dtype, w.shape, read(w.file));
   addon.planCheck(ctx, planText);
+  if (meta.sched) {
+    // two copies of the plan under the scheduler: sequences from ids.bin / offsets.bin
+    if (meta.words) addon.wordsSet(ctx, meta.words.dtype, meta.words.rows, meta.words.width, read(meta.words.file));
+    const plans = [addon.planCreate(ctx, planText), addon.planCreate(ctx, planText)];
+    for (const p of plans) for (const [id, file] of Object.entries(meta.inits)) addon.planInitBuffer(p, id, read(file));
+    const s = addon.schedCreate(plans);
+    const tw = meta.sched.typeWords ? typed(read('tw.bin'), Uint32Array) : null;
+    const r = addon.schedRun(s, typed(read('ids.bin'), Int32Array), typed(read('offsets.bin'), Float64Array), tw,
+      meta.sched.tokenBudget || 0, meta.sched.cols);
+    fs.writeFileSync(path.join(dir, 'out.bin'), Buffer.from(r.out.buffer, r.out.byteOffset, r.out.byteLength));
+    console.log(JSON.stringify({ ok: true, stats: r.stats }));
+    addon.schedDestroy(s);
+    for (const p of plans) addon.planDestroy(p);
+    addon.ctxDestroy(ctx);
+    return;
+  }
   const plan = addon.planCreate(ctx, planText);
   for (const [id, file] of Object.entries(meta.inits)) addon.planInitBuffer(plan, id, read(file));
   const tt = meta.typeIds ? typed(read('tt.bin'), Uint32Array) : null;

@@ -49,6 +49,26 @@ def export_case(dirname: str, plan: dict, weights: dict | None = None, run_input
         json.dump(meta, f)
 
 
+def export_sched_case(dirname: str, plan: dict, weights: dict, words: np.ndarray, seqs: list, type_words: np.ndarray,
+                      token_budget: int = 0) -> None:
+    """Case files for the scheduler path of run_plan.js: the plan (two copies run under kh_sched),
+    weights, the device word table and the sequences as ids + offsets."""
+    export_case(dirname, plan, weights, {"embeddings": np.zeros(1, np.float16), "mask": np.zeros(1, np.float32)})
+    with open(os.path.join(dirname, "meta.json")) as f:
+        meta = json.load(f)
+    np.ascontiguousarray(words).tofile(os.path.join(dirname, "words.bin"))
+    meta["words"] = {"file": "words.bin", "dtype": 1 if words.dtype == np.float16 else 0,
+                     "rows": int(words.shape[0]), "width": int(words.shape[1])}
+    np.concatenate([np.asarray(x, np.int32) for x in seqs]).tofile(os.path.join(dirname, "ids.bin"))
+    offs = np.zeros(len(seqs) + 1, np.float64)
+    offs[1:] = np.cumsum([len(x) for x in seqs])
+    offs.tofile(os.path.join(dirname, "offsets.bin"))
+    np.ascontiguousarray(type_words, dtype=np.uint32).tofile(os.path.join(dirname, "tw.bin"))
+    meta["sched"] = {"typeWords": True, "tokenBudget": token_budget, "cols": plan["output"]["cols"]}
+    with open(os.path.join(dirname, "meta.json"), "w") as f:
+        json.dump(meta, f)
+
+
 def run_node(dirname: str, timeout: int = 120) -> dict:
     r = subprocess.run(["node", RUNNER, dirname], capture_output=True, text=True, timeout=timeout)
     if r.returncode != 0:

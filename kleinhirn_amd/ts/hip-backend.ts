@@ -45,6 +45,12 @@ export interface KhAddon {
   // kh_scores / kh_rank: the numeric steps after the plan (src/tasks.ts, src/encoder.ts:498-544)
   scores(logits: Float32Array, cols: number, kind: number): { scores: Float32Array; index: Int32Array };
   rank(scores: Float32Array): Int32Array;
+  // kh_sched_*: packed batch scheduling over created plans (runIdsBatch, src/encoder.ts:380-436)
+  schedCreate(plans: KhHandle[]): KhHandle;
+  schedRun(s: KhHandle, ids: Int32Array, offsets: Float64Array, typeWords: Uint32Array | null, tokenBudget: number,
+    cols: number): { out: Float32Array; stats: { chunks: number; sequences: number; tokens: number; wallMs: number;
+      gpuMs: number; hostMs: number } };
+  schedDestroy(s: KhHandle): void;
 }
 
 // kh_scores kinds: single-label softmax, multi-label sigmoid, regression, L2-normalised embedding

@@ -116,3 +116,23 @@ def test_node_addon_scores_and_rank_equal_the_oracle():
     assert np.array_equal(np.array(res["s"], np.float32).reshape(9, 3), want)
     assert res["i"] == wi.tolist()
     assert res["o"] == [1, 4, 0, 2, 3]
+
+
+@pytest.mark.gpu
+def test_node_scheduler_matches_python_path():
+    """schedCreate / schedRun through the addon: two copies of a batch-4 plan run the c2 case in
+    length-ordered chunks; outputs equal the Python host's batch plan bit for bit."""
+    from kleinhirn_amd.node_case import export_sched_case
+    from kleinhirn_amd.scheduler import type_words
+    from tests.helpers import hip_outputs
+    from tests.test_gpu_models import case_and_oracle
+    case, _ = case_and_oracle("c2")
+    W = configs.storage(case.weights, True)
+    words = W.pop("embeddings.word.weight")
+    plan = build_plan(case.spec, case.head, case.length, 4, True)
+    with tempfile.TemporaryDirectory() as d:
+        export_sched_case(d, plan, W, words, case.ids, type_words(case.spec, case.ids), token_budget=700)
+        res = run_node(d)
+        got = np.fromfile(os.path.join(d, "out.bin"), dtype=np.float32).reshape(len(case.ids), -1)
+    assert res["ok"] and res["stats"]["sequences"] == len(case.ids)
+    assert np.array_equal(got, hip_outputs(case, f16=True))

@@ -203,3 +203,18 @@ def test_no_device_fails_loudly_without_fallback():
     from kleinhirn_amd.backend import HipBackend, KhError
     with pytest.raises(KhError):
         HipBackend({})
+
+
+def test_scheduler_type_words_equal_the_per_sequence_packing():
+    """The scheduler's per-token type words (vectorised position rows) equal mask_and_types'
+    words of the same sequences (src/encoder.ts:284-314)."""
+    from kleinhirn_amd import configs, inputs
+    from kleinhirn_amd.scheduler import type_words
+    for name in ("c2", "c3b"):
+        w = configs.ALL[name]()
+        ids = w.ids()[:9]
+        ids[3] = np.array([w.spec["embed"].get("padId") or 0] * 3 + list(ids[3][:5]), dtype=np.int32)
+        L = max(len(x) for x in ids)
+        _, tt = inputs.mask_and_types(w.spec, ids, L)
+        want = np.concatenate([tt[b * L:b * L + len(x)] for b, x in enumerate(ids)])
+        assert np.array_equal(type_words(w.spec, ids), want)
