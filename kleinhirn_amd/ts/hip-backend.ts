@@ -112,6 +112,11 @@ export class HipPlanRunner implements PlanRunner {
     return this.h;
   }
 
+  // the native plan, for the addon's scheduler (schedCreate)
+  get planHandle(): KhHandle {
+    return this.handle();
+  }
+
   get bytes(): number {
     return this.kh.planInfo(this.handle()).bytes;
   }
