@@ -178,8 +178,8 @@ typedef struct {
   uint64_t bytes;       /* PlanRunner.bytes: device bytes held for this plan */
   int32_t out_rows;     /* Plan.output.rows */
   int32_t out_cols;     /* Plan.output.cols */
-  int32_t launches;     /* kernel launches of one run */
-  int32_t reserved;
+  int32_t launches;     /* kernel launches of one run (of one half when split) */
+  int32_t streams;      /* 2 when the last run split the batch over two streams, else 1 */
 } kh_plan_info;
 
 int kh_plan_info_get(const kh_plan *plan, kh_plan_info *out);
@@ -197,7 +197,9 @@ int kh_upload_ids(kh_plan *plan, const int32_t *ids, size_t id_count, const floa
                   size_t mask_count, const uint32_t *type_ids, size_t type_count);
 
 /* PlanRunner.run (src/plan/executor.ts:295-297): one forward over `rows` rows (the real rows of
- * a B = 1 call, L * B for a batch plan), enqueued on the plan's stream; returns without waiting. */
+ * a B = 1 call, L * B for a batch plan), enqueued on the plan's stream; returns without waiting.
+ * A batch call with fewer than KH_SPLIT_T (environment, default 65536) valid rows runs as two
+ * halves of about equal rows on two streams (KH_NO_SPLIT=1: one stream); outputs are the same. */
 int kh_run(kh_plan *plan, int32_t rows);
 
 /* PlanRunner.readOutput (src/plan/executor.ts:398-408): waits, then writes rows * cols f32
@@ -223,6 +225,14 @@ typedef struct {
 } kh_launch_stat;
 
 int kh_profile(kh_plan *plan, int32_t rows, kh_launch_stat *out, int32_t cap, int32_t *count);
+
+/* Live per-launch timing: with tracing on, every kh_run records a HIP event pair around each of
+ * its launches on the stream that launch runs on (both halves of a split batch); kh_trace_read
+ * waits and returns the launches recorded since the last read (or kh_trace call) in launch order,
+ * in the records of kh_profile, and clears them (a null `out` only sets *count). kh_trace(plan, 0)
+ * stops recording. */
+int kh_trace(kh_plan *plan, int32_t on);
+int kh_trace_read(kh_plan *plan, kh_launch_stat *out, int32_t cap, int32_t *count);
 
 /* Packed rows (sum of valid sequence lengths) of the last run. */
 int kh_packed_rows(const kh_plan *plan, int64_t *out);

@@ -30,7 +30,7 @@ EXPORTS = [
     "kh_plan_info_get", "kh_upload", "kh_upload_ids", "kh_run", "kh_read_output", "kh_sync",
     "kh_last_run_ms", "kh_profile", "kh_packed_rows", "kh_plan_destroy", "kh_manifest_check",
     "kh_load_manifest", "kh_sha256", "kh_row_checksum", "kh_scores", "kh_read_scores", "kh_rank",
-    "kh_sched_create", "kh_sched_run", "kh_sched_destroy",
+    "kh_sched_create", "kh_sched_run", "kh_sched_destroy", "kh_trace", "kh_trace_read",
 ]
 
 # kh_scores kinds
@@ -49,7 +49,7 @@ class KhError(RuntimeError):
 class PlanInfo(ctypes.Structure):
     _fields_ = [("length", ctypes.c_int32), ("batch", ctypes.c_int32), ("markers", ctypes.c_int32),
                 ("f16", ctypes.c_int32), ("bytes", ctypes.c_uint64), ("out_rows", ctypes.c_int32),
-                ("out_cols", ctypes.c_int32), ("launches", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("out_cols", ctypes.c_int32), ("launches", ctypes.c_int32), ("streams", ctypes.c_int32)]
 
 
 class ManifestInfo(ctypes.Structure):
@@ -119,6 +119,8 @@ def lib() -> ctypes.CDLL:
         "kh_sched_create": [ctypes.POINTER(vp), i32, ctypes.POINTER(vp)],
         "kh_sched_run": [vp, vp, vp, i64, vp, i64, vp, sz, ctypes.POINTER(SchedStats)],
         "kh_sched_destroy": [vp],
+        "kh_trace": [vp, i32],
+        "kh_trace_read": [vp, ctypes.POINTER(LaunchStat), i32, ctypes.POINTER(i32)],
     }
     for name, args in sigs.items():
         fn = getattr(L, name)
@@ -274,6 +276,20 @@ class HipPlanRunner:
         arr = (LaunchStat * cap)()
         n = ctypes.c_int32()
         _check(lib().kh_profile(self.h, int(rows), arr, cap, ctypes.byref(n)))
+        return [{"name": arr[i].name.decode(), "kernel": arr[i].kernel.decode(), "ms": float(arr[i].ms),
+                 "flops": float(arr[i].flops), "bytes": float(arr[i].bytes)} for i in range(min(n.value, cap))]
+
+    def trace(self, on: bool) -> None:
+        """Record HIP events around every launch of the following runs (kh_trace)."""
+        _check(lib().kh_trace(self.h, 1 if on else 0))
+
+    def trace_read(self) -> list[dict]:
+        """The launches recorded since the last read, with their GPU ms (kh_trace_read)."""
+        n = ctypes.c_int32()
+        _check(lib().kh_trace_read(self.h, None, 0, ctypes.byref(n)))
+        cap = max(1, n.value)
+        arr = (LaunchStat * cap)()
+        _check(lib().kh_trace_read(self.h, arr, cap, ctypes.byref(n)))
         return [{"name": arr[i].name.decode(), "kernel": arr[i].kernel.decode(), "ms": float(arr[i].ms),
                  "flops": float(arr[i].flops), "bytes": float(arr[i].bytes)} for i in range(min(n.value, cap))]
 

@@ -675,18 +675,41 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
           }
         }
     }
+    // instruction order of the slab: the first step's LDS reads, then each step's MFMAs with the
+    // next step's reads between them (one read after each of the first MFMAs), so a read has a
+    // step of MFMAs to land in before its value is used
+    constexpr int NR = FM + FN, NM = FM * FN;
+    static_assert(NM >= NR, "a step needs as many MFMAs as reads to hide them");
+    __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+#pragma unroll
+    for (int kk = 0; kk < 3; kk++) {
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      if constexpr (NM > NR) __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
   };
 
-  // slab it in stage it % 2: wait for this wavefront's loads of it, then a barrier (every part
-  // landed, and the stage the next issue overwrites is no longer read)
-  for (int it = 0; it < nk; it += 2) {
+  // slab s in stage s % 2: wait for this wavefront's loads of s, then a barrier (every part
+  // landed, and the stage the next issue overwrites is no longer read). The first slab is peeled
+  // and the loop body holds two whole slabs, so the accumulators stay in place across iterations.
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  if (1 < nk) issue(1, 64);
+  slab(smem, std::true_type{});
+  int it = 1;
+  for (; it + 1 < nk; it += 2) {
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if (it + 1 < nk) issue(1, (it + 1) * 64);
-    if (it == 0) slab(smem, std::true_type{});
-    else slab(smem, std::false_type{});
-    if (it + 1 >= nk) break;
+    issue(0, (it + 1) * 64);
+    slab(smem + STAGE, std::false_type{});
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if (it + 2 < nk) issue(0, (it + 2) * 64);
+    if (it + 2 < nk) issue(1, (it + 2) * 64);
+    slab(smem, std::false_type{});
+  }
+  if (it < nk) {
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     slab(smem + STAGE, std::false_type{});
   }
 

@@ -146,6 +146,13 @@ struct Step {
   bool first_tiles = false;  // S_ATTN: only the first query tile of each sequence
 };
 
+// one traced launch: an event pair recorded around its dispatch on the stream it ran on
+struct TraceRec {
+  std::string name, kernel;
+  double flops = 0, bytes = 0;
+  hipEvent_t a = nullptr, b = nullptr;
+};
+
 struct Buffer {
   int64_t bytes = 0;
   std::string usage;
@@ -181,6 +188,21 @@ struct kh_plan {
   hipStream_t stream = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   bool ran = false;
+
+  // A small batch runs as two halves on two streams: sequences [0, split) here, [split, B) on the
+  // twin (the same plan, its own buffers and stream), so the kernels of one half fill the CUs the
+  // other half's grids leave idle. split = 0: the whole batch here.
+  std::string json;                                                    // the plan document
+  std::vector<std::pair<std::string, std::vector<uint8_t>>> init_log;  // kh_plan_init_buffer calls
+  kh_plan *twin = nullptr;
+  bool is_twin = false;
+  int split = 0;
+  hipEvent_t ev_twin = nullptr;
+
+  // live per-launch timing of kh_run (kh_trace / kh_trace_read)
+  bool tracing = false;
+  std::vector<TraceRec> trace;
+  std::vector<hipEvent_t> ev_pool;
 
   // upload staging (host, padded layout as the caller gave it)
   std::vector<uint8_t> emb_host;
@@ -871,7 +893,7 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
 
 // ---- packing ----------------------------------------------------------------------------------
 
-static void pack(kh_plan *pl, int rows) {
+static void pack(kh_plan *pl, int rows, int b_end) {
   const int L = pl->L, B = pl->B;
   std::vector<int32_t> n(B);
   for (int b = 0; b < B; b++) {
@@ -887,7 +909,7 @@ static void pack(kh_plan *pl, int rows) {
         fail(KH_EINVAL, "mask of sequence " + std::to_string(b) + " has a hole before row " + std::to_string(i) +
                             ": the HIP runner takes prefix masks");
     }
-    int cap = rows - b * L;
+    int cap = b < b_end ? rows - b * L : 0;
     cap = cap < 0 ? 0 : (cap > L ? L : cap);
     n[b] = len < cap ? len : cap;
   }
@@ -1031,6 +1053,147 @@ static void ensure_rel(kh_plan *pl) {
 static void run_steps(kh_plan *pl, const LaunchHook &hook) {
   for (const Step &s : active_steps(pl)) exec_step(pl, s, hook);
   KH_CHECK(hipGetLastError());
+}
+
+// ---- the twin: the second half of a small batch on its own stream ------------------------------
+
+static int64_t env_int(const char *name, int64_t dflt) {
+  const char *e = getenv(name);
+  return e && *e ? atoll(e) : dflt;
+}
+
+// Sequences [0, split) stay on this plan; 0 runs the batch whole. Only batch calls (rows = L * B)
+// of plans whose output rows are per sequence or per token split, and only below KH_SPLIT_T valid
+// rows (default 65536: above that one half's grids already fill the chip), with both halves holding
+// about half the rows.
+static int choose_split(const kh_plan *pl, int rows) {
+  if (pl->is_twin || pl->B < 2 || rows != pl->L * pl->B || env_int("KH_NO_SPLIT", 0)) return 0;
+  const bool per_seq = !pl->out_packed && pl->out_rows == pl->B;
+  const bool per_tok = pl->out_packed && pl->out_rows == pl->L * pl->B;
+  if (!per_seq && !per_tok) return 0;
+  std::vector<int64_t> pre(pl->B + 1, 0);
+  for (int b = 0; b < pl->B; b++) {
+    const float *m = pl->mask_host.data() + (size_t)b * pl->L;
+    int len = 0;
+    while (len < pl->L && m[len] > 0.5f) len++;
+    pre[b + 1] = pre[b] + len;
+  }
+  const int64_t T = pre[pl->B];
+  if (T < 2048 || T >= env_int("KH_SPLIT_T", 65536)) return 0;
+  int split = 1;
+  while (split < pl->B - 1 && 2 * pre[split] < T) split++;
+  if (pre[split] == 0 || pre[split] == T) return 0;
+  return split;
+}
+
+static void ensure_twin(kh_plan *pl) {
+  if (pl->twin) return;
+  kh_plan *t = nullptr;
+  int rc = kh_plan_create(pl->ctx, pl->json.data(), pl->json.size(), &t);
+  if (rc) fail(rc, std::string("twin plan: ") + kh_last_error());
+  t->is_twin = true;
+  for (const auto &in : pl->init_log) {
+    rc = kh_plan_init_buffer(t, in.first.c_str(), in.second.data(), in.second.size());
+    if (rc) {
+      const std::string m = kh_last_error();
+      kh_plan_destroy(t);
+      fail(rc, "twin plan: " + m);
+    }
+  }
+  KH_CHECK(hipEventCreateWithFlags(&pl->ev_twin, hipEventDisableTiming));
+  pl->twin = t;
+}
+
+// the twin's host arrays: sequences [split, B) of this plan's upload at slots [0, B - split)
+static void stage_twin(kh_plan *pl, int split) {
+  kh_plan *t = pl->twin;
+  const size_t L = pl->L, M = L * pl->B, moved = (size_t)(pl->B - split) * L, from = (size_t)split * L;
+  t->mask_host.assign(M, 0.f);
+  memcpy(t->mask_host.data(), pl->mask_host.data() + from, moved * 4);
+  t->tt_host.clear();
+  if (!pl->tt_host.empty()) {
+    t->tt_host.assign(M, 0u);
+    memcpy(t->tt_host.data(), pl->tt_host.data() + from, moved * 4);
+  }
+  t->by_ids = pl->by_ids;
+  if (pl->by_ids) {
+    t->ids_host.assign(M, 0);
+    memcpy(t->ids_host.data(), pl->ids_host.data() + from, moved * 4);
+  } else {
+    const size_t row = (size_t)pl->E * (pl->f16 ? 2 : 4);
+    t->emb_host.assign(M * row, 0);
+    if (pl->emb_host.size() > from * row)
+      memcpy(t->emb_host.data(), pl->emb_host.data() + from * row, std::min(moved * row, pl->emb_host.size() - from * row));
+  }
+  t->uploaded = true;
+  t->dirty = true;
+}
+
+// packs (when the upload or the split changed) and enqueues the forward of the whole batch
+static void launch_forward(kh_plan *pl, int rows, const LaunchHook &hook, bool sequential) {
+  const int split = choose_split(pl, rows);
+  if (split > 0) {
+    ensure_twin(pl);
+    if (pl->dirty || split != pl->split) stage_twin(pl, split);
+  }
+  if (pl->dirty || rows != pl->last_rows || split != pl->split) pack(pl, rows, split > 0 ? split : pl->B);
+  pl->split = split;
+  ensure_rel(pl);
+  kh_plan *t = pl->twin;
+  if (split > 0) {
+    if (t->dirty) pack(t, t->L * t->B, t->B);
+    ensure_rel(t);
+  }
+  KH_CHECK(hipEventRecord(pl->ev0, pl->stream));
+  run_steps(pl, hook);
+  if (split > 0) {
+    if (sequential) KH_CHECK(hipStreamSynchronize(pl->stream));  // profiled halves one after the other
+    run_steps(t, hook);
+    KH_CHECK(hipEventRecord(pl->ev_twin, t->stream));
+    KH_CHECK(hipStreamWaitEvent(pl->stream, pl->ev_twin, 0));
+    t->ran = true;
+  }
+  KH_CHECK(hipEventRecord(pl->ev1, pl->stream));
+  pl->ran = true;
+}
+
+static hipEvent_t take_event(kh_plan *pl) {
+  if (!pl->ev_pool.empty()) {
+    hipEvent_t e = pl->ev_pool.back();
+    pl->ev_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e;
+  KH_CHECK(hipEventCreate(&e));
+  return e;
+}
+
+// the traced launches of kh_run go to pl->trace (both halves of a split batch)
+static LaunchHook trace_hook(kh_plan *pl) {
+  return [pl](const Step &s, const char *k, double fl, double by, bool begin) {
+    if (begin) {
+      TraceRec r;
+      r.name = s.name;
+      r.kernel = k;
+      r.flops = fl;
+      r.bytes = by;
+      r.a = take_event(pl);
+      r.b = take_event(pl);
+      pl->trace.push_back(r);
+      g_launch_events.start = r.a;
+      g_launch_events.stop = r.b;
+    } else {
+      g_launch_events = LaunchEvents();
+    }
+  };
+}
+
+static void release_trace(kh_plan *pl) {
+  for (TraceRec &r : pl->trace) {
+    pl->ev_pool.push_back(r.a);
+    pl->ev_pool.push_back(r.b);
+  }
+  pl->trace.clear();
 }
 
 static void latch(kh_ctx *ctx, const Error &e) {
@@ -1344,6 +1507,7 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
   Parsed pp = parse_plan(plan_json, len);
   std::unique_ptr<kh_plan> pl(new kh_plan());
   pl->ctx = ctx;
+  pl->json.assign(plan_json, len);
   pl->f16 = pp.root.at("f16").kind == Json::Bool && pp.root.at("f16").b;
   pl->L = (int)pp.root.at("length").integer();
   pl->B = (int)pp.root.at("batch").integer();
@@ -1461,10 +1625,7 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
   KH_API_END
 }
 
-int kh_plan_init_buffer(kh_plan *plan, const char *id, const void *data, size_t bytes) {
-  KH_API_BEGIN
-  if (!plan || !id) fail(KH_EINVAL, "null argument");
-  require_live(plan->ctx);
+static void init_buffer(kh_plan *plan, const char *id, const void *data, size_t bytes) {
   auto it = plan->bufs.find(id);
   if (it == plan->bufs.end()) fail(KH_EINVAL, std::string("plan buffer ") + id + " missing");
   Buffer &b = it->second;
@@ -1492,13 +1653,31 @@ int kh_plan_init_buffer(kh_plan *plan, const char *id, const void *data, size_t 
     }
     plan->d_bucket.alloc(plan->bucket_host.size() * 4);
     KH_CHECK(hipMemcpy(plan->d_bucket.p, plan->bucket_host.data(), plan->bucket_host.size() * 4, hipMemcpyHostToDevice));
-    return KH_OK;
+    return;
   }
   if (b.mem) KH_CHECK(hipMemcpy(b.mem->p, data, bytes, hipMemcpyHostToDevice));
   if (sid == plan->prune_markers) {
     memcpy(plan->markers_shadow.data(), data, bytes);
     check_markers(plan);
   }
+}
+
+
+int kh_plan_init_buffer(kh_plan *plan, const char *id, const void *data, size_t bytes) {
+  KH_API_BEGIN
+  if (!plan || !id) fail(KH_EINVAL, "null argument");
+  require_live(plan->ctx);
+  init_buffer(plan, id, data, bytes);
+  // kept for the twin (created at the first split run), and applied to it when it exists
+  std::vector<uint8_t> copy((const uint8_t *)data, (const uint8_t *)data + bytes);
+  bool logged = false;
+  for (auto &in : plan->init_log)
+    if (in.first == id) {
+      in.second = copy;
+      logged = true;
+    }
+  if (!logged) plan->init_log.push_back({id, copy});
+  if (plan->twin) init_buffer(plan->twin, id, data, bytes);
   KH_API_END
 }
 
@@ -1513,11 +1692,15 @@ int kh_plan_info_get(const kh_plan *plan, kh_plan_info *out) {
   uint64_t bytes = 0;
   for (const auto &kv : plan->bufs)
     if (kv.second.mem) bytes += kv.second.mem->bytes;
+  if (plan->twin)
+    for (const auto &kv : plan->twin->bufs)
+      if (kv.second.mem) bytes += kv.second.mem->bytes;
 
   out->bytes = bytes;
   out->out_rows = plan->out_rows;
   out->out_cols = plan->out_cols;
   out->launches = (int32_t)active_steps(plan).size();
+  out->streams = plan->split > 0 ? 2 : 1;
   KH_API_END
 }
 
@@ -1578,13 +1761,14 @@ int kh_run(kh_plan *plan, int32_t rows) {
     fail(KH_EINVAL, std::to_string(rows) + " rows, the plan has " + std::to_string(plan->L * plan->B));
   if (!plan->uploaded) fail(KH_EINVAL, "run before upload");
   try {
-    if (plan->dirty || rows != plan->last_rows) pack(plan, rows);
-    ensure_rel(plan);
-    KH_CHECK(hipEventRecord(plan->ev0, plan->stream));
-    run_steps(plan, nullptr);
-    KH_CHECK(hipEventRecord(plan->ev1, plan->stream));
-    plan->ran = true;
+    if (plan->tracing) {
+      launch_forward(plan, rows, trace_hook(plan), false);
+      g_launch_events = LaunchEvents();
+    } else {
+      launch_forward(plan, rows, nullptr, false);
+    }
   } catch (const Error &e) {
+    g_launch_events = LaunchEvents();
     latch(plan->ctx, e);
     throw;
   }
@@ -1597,6 +1781,7 @@ int kh_sync(kh_plan *plan) {
   require_live(plan->ctx);
   try {
     KH_CHECK(hipStreamSynchronize(plan->stream));
+    if (plan->twin) KH_CHECK(hipStreamSynchronize(plan->twin->stream));
   } catch (const Error &e) {
     latch(plan->ctx, e);
     throw;
@@ -1616,8 +1801,39 @@ int kh_last_run_ms(kh_plan *plan, float *ms) {
 int kh_packed_rows(const kh_plan *plan, int64_t *out) {
   KH_API_BEGIN
   if (!plan || !out) fail(KH_EINVAL, "null argument");
-  *out = plan->T;
+  *out = plan->T + (plan->split > 0 && plan->twin ? plan->twin->T : 0);
   KH_API_END
+}
+
+// the plan's own output (its sequences only) in the plan's output layout
+static void read_into(kh_plan *plan, float *out, size_t n) {
+  Buffer &b = plan->bufs.at(plan->out_buf);
+  const size_t es = plan->f16 ? 2 : 4;
+  const int cols = plan->out_cols;
+  if (!plan->out_packed) {
+    std::vector<uint8_t> raw(n * es);
+    KH_CHECK(hipMemcpyAsync(raw.data(), b.mem->p, n * es, hipMemcpyDeviceToHost, plan->stream));
+    KH_CHECK(hipStreamSynchronize(plan->stream));
+    // sequences without a valid row: zero output (the reference computes them from padding)
+    for (size_t i = 0; i < n; i++) out[i] = plan->f16 ? (float)((const _Float16 *)raw.data())[i] : ((const float *)raw.data())[i];
+    if (plan->out_rows == plan->B)
+      for (int bb = 0; bb < plan->B; bb++)
+        if (plan->cu[bb + 1] == plan->cu[bb]) memset(out + (size_t)bb * cols, 0, (size_t)cols * 4);
+  } else {
+    // token rows: packed row cu[b] + i goes to b * L + i; rows past a sequence are zero
+    const int64_t T = plan->T;
+    std::vector<uint8_t> raw((size_t)std::max<int64_t>(T, 1) * cols * es);
+    if (T > 0) KH_CHECK(hipMemcpyAsync(raw.data(), b.mem->p, (size_t)T * cols * es, hipMemcpyDeviceToHost, plan->stream));
+    KH_CHECK(hipStreamSynchronize(plan->stream));
+    memset(out, 0, n * 4);
+    for (int bb = 0; bb < plan->B; bb++)
+      for (int i = 0; i < plan->cu[bb + 1] - plan->cu[bb]; i++) {
+        const size_t src = ((size_t)plan->cu[bb] + i) * cols, dst = ((size_t)bb * plan->L + i) * cols;
+        if (dst + cols > n) break;
+        for (int c = 0; c < cols; c++)
+          out[dst + c] = plan->f16 ? (float)((const _Float16 *)raw.data())[src + c] : ((const float *)raw.data())[src + c];
+      }
+  }
 }
 
 int kh_read_output(kh_plan *plan, float *out, size_t count) {
@@ -1628,32 +1844,14 @@ int kh_read_output(kh_plan *plan, float *out, size_t count) {
   const size_t n = (size_t)plan->out_rows * plan->out_cols;
   if (count < n) fail(KH_EINVAL, "output holds " + std::to_string(n) + " values, the array " + std::to_string(count));
   try {
-    Buffer &b = plan->bufs.at(plan->out_buf);
-    const size_t es = plan->f16 ? 2 : 4;
-    const int cols = plan->out_cols;
-    if (!plan->out_packed) {
-      std::vector<uint8_t> raw(n * es);
-      KH_CHECK(hipMemcpyAsync(raw.data(), b.mem->p, n * es, hipMemcpyDeviceToHost, plan->stream));
-      KH_CHECK(hipStreamSynchronize(plan->stream));
-      // sequences without a valid row: zero output (the reference computes them from padding)
-      for (size_t i = 0; i < n; i++) out[i] = plan->f16 ? (float)((const _Float16 *)raw.data())[i] : ((const float *)raw.data())[i];
-      if (plan->out_rows == plan->B)
-        for (int bb = 0; bb < plan->B; bb++)
-          if (plan->cu[bb + 1] == plan->cu[bb]) memset(out + (size_t)bb * cols, 0, (size_t)cols * 4);
-    } else {
-      // token rows: packed row cu[b] + i goes to b * L + i; rows past a sequence are zero
-      const int64_t T = plan->T;
-      std::vector<uint8_t> raw((size_t)std::max<int64_t>(T, 1) * cols * es);
-      if (T > 0) KH_CHECK(hipMemcpyAsync(raw.data(), b.mem->p, (size_t)T * cols * es, hipMemcpyDeviceToHost, plan->stream));
-      KH_CHECK(hipStreamSynchronize(plan->stream));
-      memset(out, 0, n * 4);
-      for (int bb = 0; bb < plan->B; bb++)
-        for (int i = 0; i < plan->cu[bb + 1] - plan->cu[bb]; i++) {
-          const size_t src = ((size_t)plan->cu[bb] + i) * cols, dst = ((size_t)bb * plan->L + i) * cols;
-          if (dst + cols > n) break;
-          for (int c = 0; c < cols; c++)
-            out[dst + c] = plan->f16 ? (float)((const _Float16 *)raw.data())[src + c] : ((const float *)raw.data())[src + c];
-        }
+    read_into(plan, out, n);
+    if (plan->split > 0 && plan->twin) {
+      // the twin's sequence j is sequence split + j of the batch
+      std::vector<float> t(n);
+      read_into(plan->twin, t.data(), n);
+      const size_t per = plan->out_packed ? (size_t)plan->L * plan->out_cols : (size_t)plan->out_cols;
+      const size_t moved = (size_t)(plan->B - plan->split) * per;
+      memcpy(out + (size_t)plan->split * per, t.data(), moved * 4);
     }
   } catch (const Error &e) {
     latch(plan->ctx, e);
@@ -1708,8 +1906,6 @@ int kh_profile(kh_plan *plan, int32_t rows, kh_launch_stat *out, int32_t cap, in
   require_live(plan->ctx);
   if (!plan->uploaded) fail(KH_EINVAL, "profile before upload");
   if (rows < 1 || rows > plan->L * plan->B) fail(KH_EINVAL, "rows outside the plan");
-  if (plan->dirty || rows != plan->last_rows) pack(plan, rows);
-  ensure_rel(plan);
   struct Rec {
     std::string name, kernel;
     double flops, bytes;
@@ -1733,11 +1929,8 @@ int kh_profile(kh_plan *plan, int32_t rows, kh_launch_stat *out, int32_t cap, in
         g_launch_events = LaunchEvents();
       }
     };
-    KH_CHECK(hipEventRecord(plan->ev0, plan->stream));
-    run_steps(plan, hook);
-    KH_CHECK(hipEventRecord(plan->ev1, plan->stream));
+    launch_forward(plan, rows, hook, true);
     KH_CHECK(hipStreamSynchronize(plan->stream));
-    plan->ran = true;
   } catch (const Error &e) {
     g_launch_events = LaunchEvents();
     for (auto &r : recs) {
@@ -1767,13 +1960,51 @@ int kh_profile(kh_plan *plan, int32_t rows, kh_launch_stat *out, int32_t cap, in
   KH_API_END
 }
 
+int kh_trace(kh_plan *plan, int32_t on) {
+  KH_API_BEGIN
+  if (!plan) fail(KH_EINVAL, "null plan");
+  require_live(plan->ctx);
+  KH_CHECK(hipStreamSynchronize(plan->stream));
+  if (plan->twin) KH_CHECK(hipStreamSynchronize(plan->twin->stream));
+  release_trace(plan);
+  plan->tracing = on != 0;
+  KH_API_END
+}
+
+int kh_trace_read(kh_plan *plan, kh_launch_stat *out, int32_t cap, int32_t *count) {
+  KH_API_BEGIN
+  if (!plan || !count) fail(KH_EINVAL, "null argument");
+  require_live(plan->ctx);
+  KH_CHECK(hipStreamSynchronize(plan->stream));
+  if (plan->twin) KH_CHECK(hipStreamSynchronize(plan->twin->stream));
+  *count = (int32_t)plan->trace.size();
+  for (size_t i = 0; i < plan->trace.size() && (int32_t)i < cap && out; i++) {
+    const TraceRec &r = plan->trace[i];
+    float ms = 0;
+    KH_CHECK(hipEventElapsedTime(&ms, r.a, r.b));
+    kh_launch_stat &o = out[i];
+    memset(&o, 0, sizeof(o));
+    snprintf(o.name, sizeof(o.name), "%s", r.name.c_str());
+    snprintf(o.kernel, sizeof(o.kernel), "%s", r.kernel.c_str());
+    o.ms = ms;
+    o.flops = r.flops;
+    o.bytes = r.bytes;
+  }
+  if (out) release_trace(plan);  // a null array only counts
+  KH_API_END
+}
+
 int kh_plan_destroy(kh_plan *plan) {
   KH_API_BEGIN
   if (plan) {
     (void)hipSetDevice(plan->ctx->device);
+    if (plan->twin) kh_plan_destroy(plan->twin);
+    if (plan->ev_twin) (void)hipEventDestroy(plan->ev_twin);
     if (plan->stream) (void)hipStreamSynchronize(plan->stream);
     if (plan->ev0) (void)hipEventDestroy(plan->ev0);
     if (plan->ev1) (void)hipEventDestroy(plan->ev1);
+    release_trace(plan);
+    for (hipEvent_t e : plan->ev_pool) (void)hipEventDestroy(e);
     hipStream_t s = plan->stream;
     delete plan;
     if (s) (void)hipStreamDestroy(s);

@@ -290,6 +290,7 @@ static napi_value plan_info(napi_env env, napi_callback_info info) {
   SET("outRows", pi.out_rows);
   SET("outCols", pi.out_cols);
   SET("launches", pi.launches);
+  SET("streams", pi.streams);
 #undef SET
   return o;
 }

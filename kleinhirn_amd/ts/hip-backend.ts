@@ -32,7 +32,7 @@ export interface KhAddon {
   planCreate(ctx: KhHandle, json: string): KhHandle;
   planInitBuffer(plan: KhHandle, id: string, data: ArrayBufferView): void;
   planInfo(plan: KhHandle): { length: number; batch: number; markers: number; f16: number; bytes: number;
-    outRows: number; outCols: number; launches: number };
+    outRows: number; outCols: number; launches: number; streams: number };
   planDestroy(plan: KhHandle): void;
   upload(plan: KhHandle, embeddings: ArrayBufferView, mask: Float32Array, typeIds: Uint32Array | null): void;
   uploadIds(plan: KhHandle, ids: Int32Array, mask: Float32Array, typeIds: Uint32Array | null): void;
