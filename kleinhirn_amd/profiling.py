@@ -28,6 +28,7 @@ FAMILIES = [
     ("attn_kernel", "attention"),
     ("embln_kernel", "embln"),
     ("layernorm_kernel", "layernorm"),
+    ("layernorm_rows_kernel", "layernorm"),
     ("add_vec_kernel", "add"),
     ("add_kernel", "add"),
     ("geglu_kernel", "geglu"),
