@@ -589,7 +589,7 @@ __device__ __forceinline__ rsrc_t panel_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-template <int BM, int BN, int WM, int WN, int ACT, int EPI>
+template <int BM, int BN, int WM, int WN, int ACT, int EPI, int STAGES>
 __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, int tiles_n) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
@@ -678,39 +678,61 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
     // instruction order of the slab: the first step's LDS reads, then each step's MFMAs with the
     // next step's reads between them (one read after each of the first MFMAs), so a read has a
     // step of MFMAs to land in before its value is used
+    // (tiles whose steps have fewer MFMAs than reads keep the compiler's order)
     constexpr int NR = FM + FN, NM = FM * FN;
-    static_assert(NM >= NR, "a step needs as many MFMAs as reads to hide them");
-    __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+    if constexpr (NM >= NR) {
+      __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
 #pragma unroll
-    for (int kk = 0; kk < 3; kk++) {
+      for (int kk = 0; kk < 3; kk++) {
 #pragma unroll
-      for (int r = 0; r < NR; r++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        for (int r = 0; r < NR; r++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if constexpr (NM > NR) __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
       }
-      if constexpr (NM > NR) __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
   };
 
-  // slab s in stage s % 2: wait for this wavefront's loads of s, then a barrier (every part
-  // landed, and the stage the next issue overwrites is no longer read). The first slab is peeled
-  // and the loop body holds two whole slabs, so the accumulators stay in place across iterations.
-  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  if (1 < nk) issue(1, 64);
-  slab(smem, std::true_type{});
-  int it = 1;
-  for (; it + 1 < nk; it += 2) {
+  if constexpr (STAGES == 2) {
+    // slab s in stage s % 2: wait for this wavefront's loads of s, then a barrier (every part
+    // landed, and the stage the next issue overwrites is no longer read). The first slab is peeled
+    // and the loop body holds two whole slabs, so the accumulators stay in place across iterations.
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    issue(0, (it + 1) * 64);
-    slab(smem + STAGE, std::false_type{});
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if (it + 2 < nk) issue(1, (it + 2) * 64);
-    slab(smem, std::false_type{});
-  }
-  if (it < nk) {
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    slab(smem + STAGE, std::false_type{});
+    if (1 < nk) issue(1, 64);
+    slab(smem, std::true_type{});
+    int it = 1;
+    for (; it + 1 < nk; it += 2) {
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      issue(0, (it + 1) * 64);
+      slab(smem + STAGE, std::false_type{});
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      if (it + 2 < nk) issue(1, (it + 2) * 64);
+      slab(smem, std::false_type{});
+    }
+    if (it < nk) {
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      slab(smem + STAGE, std::false_type{});
+    }
+  } else {
+    // STAGES - 1 slabs in flight (short-M products, where the chain of slabs is the latency): at
+    // slab s the loads of at most STAGES - 2 later slabs may be outstanding, P per slab per
+    // wavefront; near the end fewer were issued, so the wait is for all of them
+    static_assert((STAGES - 2) * P <= 63, "vmcnt counts up to 63 loads");
+    for (int i = 1; i < STAGES - 1 && i < nk; i++) issue(i, i * 64);
+    auto wait_for = [&](int sl) {
+      if (sl + STAGES - 2 < nk) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((STAGES - 2) * P) : "memory");
+      else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    wait_for(0);
+    if (STAGES - 1 < nk) issue(STAGES - 1, (STAGES - 1) * 64);
+    slab(smem, std::true_type{});
+    for (int it = 1; it < nk; it++) {
+      wait_for(it);
+      if (it + STAGES - 1 < nk) issue((it + STAGES - 1) % STAGES, (it + STAGES - 1) * 64);
+      slab(smem + (it % STAGES) * STAGE, std::false_type{});
+    }
   }
 
   // epilogue: acc[i][j][4 q + e] is C[m0 + arow + 32 i][n0 + wn TN + 32 j + 8 q + 4 lg + e]; the
@@ -799,11 +821,11 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
 }
 
 // (the body is a device function: the buffer-resource type exists only in device compilation)
-template <int BM, int BN, int WM, int WN, int ACT, int EPI>
+template <int BM, int BN, int WM, int WN, int ACT, int EPI, int STAGES>
 __global__ void __launch_bounds__(64 * WM * WN)
-__attribute__((amdgpu_waves_per_eu(waves_per_simd<BM, BN, WM, WN, 2>(), waves_per_simd<BM, BN, WM, WN, 2>())))
+__attribute__((amdgpu_waves_per_eu(waves_per_simd<BM, BN, WM, WN, STAGES>(), waves_per_simd<BM, BN, WM, WN, STAGES>())))
 gemm_lean_kernel(GemmArgs g, int tiles_m, int tiles_n) {
-  gemm_lean_body<BM, BN, WM, WN, ACT, EPI>(g, tiles_m, tiles_n);
+  gemm_lean_body<BM, BN, WM, WN, ACT, EPI, STAGES>(g, tiles_m, tiles_n);
 }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -842,25 +864,26 @@ void launch_persist(const GemmArgs &g, hipStream_t s, int blocks_per_cu) {
 }
 
 
-template <int BM, int BN, int WM, int WN, int ACT, int EPI>
+template <int BM, int BN, int WM, int WN, int ACT, int EPI, int STAGES>
 void launch_lean_epi(const GemmArgs &g, hipStream_t s) {
   const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
-  constexpr int smem = 2 * (BM + BN) * 128;
+  constexpr int smem = STAGES * (BM + BN) * 128;
   static bool configured = false;
   if (!configured) {
-    set_smem(gemm_lean_kernel<BM, BN, WM, WN, ACT, EPI>, smem);
+    set_smem(gemm_lean_kernel<BM, BN, WM, WN, ACT, EPI, STAGES>, smem);
     configured = true;
   }
-  launch((gemm_lean_kernel<BM, BN, WM, WN, ACT, EPI>), dim3(tm * tn), dim3(64 * WM * WN), smem, s, g, tm, tn);
+  launch((gemm_lean_kernel<BM, BN, WM, WN, ACT, EPI, STAGES>), dim3(tm * tn), dim3(64 * WM * WN), smem, s, g, tm,
+         tn);
 }
 
-template <int BM, int BN, int WM, int WN, int ACT>
+template <int BM, int BN, int WM, int WN, int ACT, int STAGES = 2>
 void launch_lean(const GemmArgs &g, hipStream_t s) {
   switch (g.epi) {
-    case EPI_GEGLU: launch_lean_epi<BM, BN, WM, WN, ACT, EPI_GEGLU>(g, s); break;
-    case EPI_ROPE: launch_lean_epi<BM, BN, WM, WN, ACT, EPI_ROPE>(g, s); break;
-    case EPI_RESADD: launch_lean_epi<BM, BN, WM, WN, ACT, EPI_RESADD>(g, s); break;
-    default: launch_lean_epi<BM, BN, WM, WN, ACT, EPI_NONE>(g, s); break;
+    case EPI_GEGLU: launch_lean_epi<BM, BN, WM, WN, ACT, EPI_GEGLU, STAGES>(g, s); break;
+    case EPI_ROPE: launch_lean_epi<BM, BN, WM, WN, ACT, EPI_ROPE, STAGES>(g, s); break;
+    case EPI_RESADD: launch_lean_epi<BM, BN, WM, WN, ACT, EPI_RESADD, STAGES>(g, s); break;
+    default: launch_lean_epi<BM, BN, WM, WN, ACT, EPI_NONE, STAGES>(g, s); break;
   }
 }
 
@@ -895,7 +918,8 @@ static int64_t lean_cost(const GemmArgs &g, int bm, int bn) {
 
 // Tile configurations. Lean f16 kernel: 8 = 192x128 (4 wavefronts of 96x64, two blocks per CU),
 // 9 = 192x256 (8 wavefronts of 96x64), 10 = 128x128 (4 of 64x64), 11 = 64x64 (1), 12 = 128x384
-// (8 of 64x96). DMA kernel: 0 = 256x256 (8 of
+// (8 of 64x96), 13 = 64x64 (4 of 32x32) with 8 slab stages, 7 slabs in flight (a few hundred rows:
+// the slab chain is the latency). DMA kernel: 0 = 256x256 (8 of
 // 128x64, 2 stages), 1 = 256x128 (4 of 128x64, 3 stages), 2 = 128x128 (4 of 64x64, 4 stages),
 // 3 = 128x128 (4 of 64x64, 2 stages, two blocks per CU), 4 = 256x256 (4 of 128x128); persistent
 // 5/6/7. KH_GEMM_TILE forces one (tuning runs).
@@ -903,13 +927,13 @@ int pick_tile(const GemmArgs &g, bool lean) {
   const char *e = getenv("KH_GEMM_TILE");
   const int forced = e ? atoi(e) : -1;
   // (a fused step runs in the lean kernel only)
-  if (forced >= 0 && forced <= 12 && (forced < 8 ? g.epi == EPI_NONE : lean)) return forced;
+  if (forced >= 0 && forced <= 13 && (forced < 8 ? g.epi == EPI_NONE : lean)) return forced;
   // measured on MI355X (f16, random data, encoder shapes M = 13k .. 1.2M): 192x128 leads in
   // general; 192x256 where N is a multiple of 256 and either narrow (N <= 768: one round of tiles
   // at M ~ 13k) or fed by a short K (<= 384, where the epilogue weighs most)
   // (a few hundred rows, e.g. a pooled head: 64 x 64 tiles, enough of them to spread over CUs)
   if (lean) {
-    if (g.M <= 1024) return 11;
+    if (g.M <= 1024) return 13;
     const int base = g.N % 256 == 0 && (g.N <= 768 || g.K <= 384) ? 9 : 8;
     // a row count just past a whole round of 192-row tiles (M = 16384: 86 row tiles) leaves the
     // last round nearly empty; 128 x 384 tiles divide such shapes into whole rounds
@@ -938,6 +962,7 @@ void launch_act(const GemmArgs &g, hipStream_t s) {
       case 10: launch_lean<128, 128, 2, 2, ACT>(g, s); return;
       case 11: launch_lean<64, 64, 1, 1, ACT>(g, s); return;
       case 12: launch_lean<128, 384, 2, 4, ACT>(g, s); return;
+      case 13: launch_lean<64, 64, 2, 2, ACT, 8>(g, s); return;
       default: break;
     }
   }
