@@ -20,6 +20,8 @@
 // pos_query rows x the sub-tile's K), parks them in its own LDS scratch (row pitch 68 floats, so
 // the diagonal reads of one register across lanes hit distinct banks) and adds each score's two
 // entries from there. The position tables are read from L2; no [T, H, buckets] array exists.
+#include <type_traits>
+
 #include "kernels.h"
 #include "device.h"
 
@@ -51,8 +53,9 @@ struct AttnMfma<float> {
   }
 };
 
-// Four wavefronts per SIMD on the standard path: short sequences are latency-bound.
-template <typename T, int D, bool REL>
+// Four wavefronts per SIMD on the standard path: short sequences are latency-bound. WIN: a sliding
+// window (a.window > 0) bounds the keys of each query.
+template <typename T, int D, bool REL, bool WIN>
 __global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(REL ? 1 : 4, 8)))
 attn_kernel(AttnArgs a, Packing p) {
   typedef AttnMfma<T> MF;
@@ -98,7 +101,7 @@ attn_kernel(AttnArgs a, Packing p) {
 
   // key range of this tile: the window around [q0, q0 + QT) or the whole sequence
   int klo = 0, khi = n;
-  if (a.window > 0) {
+  if (WIN) {
     klo = q0 - a.window > 0 ? q0 - a.window : 0;
     const int e = q0 + QT + a.window;
     khi = e < n ? e : n;
@@ -164,7 +167,9 @@ attn_kernel(AttnArgs a, Packing p) {
     // Mask and maximum on the raw scores; the scale (in base 2: scale * log2 e, so exp2 gives the
     // same weights as exp) enters once, inside the exponent. Register r of sub-tile kt is key
     // kb + 32 kt + jl(r) with jl(r) a constant, so the key-range mask is one compare per score
-    // against a per-lane limit; window bounds add two.
+    // against a limit; window bounds add two. A sub-tile wholly inside the sequence (and no
+    // window) needs no mask. Lanes of queries past the sequence (the last query tile) compute on
+    // a clamped query and are never stored; the maximum exchange pairs lanes of one query only.
     const float scale2 = a.scale * 1.4426950408889634f;
     float tmax = -INFINITY;
 #pragma unroll
@@ -218,28 +223,37 @@ attn_kernel(AttnArgs a, Packing p) {
         p2cW = p2cw - mlo;
       }
       const int k0 = kb + kt * 32;
-      const int lim = (qvalid ? khi : k0) - k0;             // keys jl < lim exist
-      const int wlo = qi - a.window - k0, whi = qi + a.window - k0;
+      auto scores = [&](auto masked_t) {
+        constexpr bool MASKED = decltype(masked_t)::value;
+        [[maybe_unused]] const int lim = khi - k0;  // keys jl < lim exist
+        [[maybe_unused]] const int wlo = qi - a.window - k0, whi = qi + a.window - k0;
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int jl = 8 * (r >> 2) + 4 * g + (r & 3);
-        bool ok = jl < lim;
-        if (a.window > 0) ok = ok && jl >= wlo && jl <= whi;
-        float v = sc[kt][r];
-        if constexpr (REL) {
-          // gathered unconditionally (no branch per score): indices clamped into the tables, the
-          // masked pairs' values are discarded below
-          int di = qi - (k0 + jl) + a.lmax - 1;
-          di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
-          int mm = sBucket[di] - mlo;
-          mm = mm < 0 ? 0 : (mm > 63 ? 63 : mm);
-          v = v + c2pW[mlo + mm];
-          v = v + p2cW[jl * RP + mlo + mm];
+        for (int r = 0; r < 16; r++) {
+          const int jl = 8 * (r >> 2) + 4 * g + (r & 3);
+          float v = sc[kt][r];
+          if constexpr (REL) {
+            // gathered unconditionally (no branch per score): indices clamped into the tables,
+            // the masked pairs' values are discarded below
+            int di = qi - (k0 + jl) + a.lmax - 1;
+            di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
+            int mm = sBucket[di] - mlo;
+            mm = mm < 0 ? 0 : (mm > 63 ? 63 : mm);
+            v = v + c2pW[mlo + mm];
+            v = v + p2cW[jl * RP + mlo + mm];
+          }
+          if constexpr (MASKED) {
+            bool ok = jl < lim;
+            if constexpr (WIN) ok = ok && jl >= wlo && jl <= whi;
+            v = ok ? v : -INFINITY;
+          }
+          sc[kt][r] = v;
+          tmax = fmaxf(tmax, v);
         }
-        v = ok ? v : -INFINITY;
-        sc[kt][r] = v;
-        tmax = fmaxf(tmax, v);
-      }
+      };
+      // (the relative path keeps one masked body: two copies of its gathers cost more than the
+      // compares they save)
+      if (REL || WIN || k0 + 32 > khi) scores(std::true_type{});
+      else scores(std::false_type{});
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
     const float m_new = fmaxf(m_run, tmax * scale2);
@@ -322,11 +336,17 @@ attn_kernel(AttnArgs a, Packing p) {
   }
 }
 
+template <typename T, bool REL, bool WIN>
+void launch_w(const AttnArgs &a, const Packing &p, hipStream_t s) {
+  dim3 grid((unsigned)a.ntiles, (unsigned)a.H);
+  if (a.D == 64) launch((attn_kernel<T, 64, REL, WIN>), grid, dim3(128), 0, s, a, p);
+  else launch((attn_kernel<T, 32, REL, WIN>), grid, dim3(128), 0, s, a, p);
+}
+
 template <typename T, bool REL>
 void launch_t(const AttnArgs &a, const Packing &p, hipStream_t s) {
-  dim3 grid((unsigned)a.ntiles, (unsigned)a.H);
-  if (a.D == 64) launch((attn_kernel<T, 64, REL>), grid, dim3(128), 0, s, a, p);
-  else launch((attn_kernel<T, 32, REL>), grid, dim3(128), 0, s, a, p);
+  if (a.window > 0) launch_w<T, REL, true>(a, p, s);
+  else launch_w<T, REL, false>(a, p, s);
 }
 
 }  // namespace
