@@ -934,6 +934,13 @@ int pick_tile(const GemmArgs &g, bool lean) {
   // (a few hundred rows, e.g. a pooled head: 64 x 64 tiles, enough of them to spread over CUs)
   if (lean) {
     if (g.M <= 1024) return 13;
+    // very many rows (c5's 1.2M): per-tile efficiency decides, measured on the 384-wide models:
+    // 128 x 384 for 384- and 768-wide outputs (one column tile: each A band is read once), 192 x 256
+    // for wider ones fed by a short K
+    if (g.M >= 524288) {
+      if (g.N % 384 == 0 && g.N <= 768) return 12;
+      if (g.N > 768 && g.N % 128 == 0 && g.K <= 384) return 9;
+    }
     const int base = g.N % 256 == 0 && (g.N <= 768 || g.K <= 384) ? 9 : 8;
     // a row count just past a whole round of 192-row tiles (M = 16384: 86 row tiles) leaves the
     // last round nearly empty; 128 x 384 tiles divide such shapes into whole rounds
