@@ -198,6 +198,9 @@ struct kh_plan {
   bool is_twin = false;
   int split = 0;
   hipEvent_t ev_twin = nullptr;
+  // choose_split's answer for the current upload, row count and switches (-1: not computed)
+  int split_memo = -1, split_memo_rows = -1;
+  int64_t split_memo_env = -1;
 
   // live per-launch timing of kh_run (kh_trace / kh_trace_read)
   bool tracing = false;
@@ -1131,7 +1134,14 @@ static void stage_twin(kh_plan *pl, int split) {
 
 // packs (when the upload or the split changed) and enqueues the forward of the whole batch
 static void launch_forward(kh_plan *pl, int rows, const LaunchHook &hook, bool sequential) {
-  const int split = choose_split(pl, rows);
+  // the split depends on the upload (dirty), the row count and the two switches
+  const int64_t env = env_int("KH_NO_SPLIT", 0) * 1000003 + env_int("KH_SPLIT_T", 65536);
+  if (pl->dirty || pl->split_memo < 0 || rows != pl->split_memo_rows || env != pl->split_memo_env) {
+    pl->split_memo = choose_split(pl, rows);
+    pl->split_memo_rows = rows;
+    pl->split_memo_env = env;
+  }
+  const int split = pl->split_memo;
   if (split > 0) {
     ensure_twin(pl);
     if (pl->dirty || split != pl->split) stage_twin(pl, split);
