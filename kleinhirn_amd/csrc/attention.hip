@@ -14,12 +14,12 @@
 // least itself and the normaliser is positive.
 //
 // DeBERTa relative attention adds q_i . pos_key[m] + k_j . pos_query[m] with m = bucket(i - j) to
-// q_i . k_j before the scale (src/wasm/plan.ts:791-840). Buckets are monotone in i - j, so the 32
-// queries of a wavefront and a 32-key sub-tile reach at most 63 consecutive buckets: per sub-tile
-// the wavefront computes both terms for those 64 position rows on MFMA (pos_key rows x its Q,
-// pos_query rows x the sub-tile's K), parks them in its own LDS scratch (row pitch 68 floats, so
-// the diagonal reads of one register across lanes hit distinct banks) and adds each score's two
-// entries from there. The position tables are read from L2; no [T, H, buckets] array exists.
+// q_i . k_j before the scale (src/wasm/plan.ts:791-840). The 32 queries of a wavefront and a
+// 32-key sub-tile span 63 distances i - j: per sub-tile the wavefront computes both terms for the
+// position rows of those distances (row r: bucket(dlo + r)) on MFMA (pos_key rows x its Q,
+// pos_query rows x the sub-tile's K), parks them in its own LDS scratch (row pitch 68 floats) and
+// adds each score's two entries from there, at offsets fixed by the score's register. The
+// position tables are read from L2; no [T, H, buckets] array exists.
 #include <type_traits>
 
 #include "kernels.h"
@@ -174,23 +174,23 @@ attn_kernel(AttnArgs a, Packing p) {
     float tmax = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
-      [[maybe_unused]] int mlo = 0;
       [[maybe_unused]] const float *c2pW = nullptr;
       [[maybe_unused]] const float *p2cW = nullptr;
       if constexpr (REL) {
-        // buckets reachable from this wavefront's queries and sub-tile kt's keys
+        // the sub-tile's distances i - j run over dlo .. dlo + 62: row r of the scratch holds the
+        // terms of distance dlo + r, computed from the position rows of bucket(dlo + r), so a
+        // score's two terms sit at fixed offsets from per-lane bases (no bucket lookup per score)
         const int kj0 = kb + kt * 32, qw0 = q0 + w * 32;
-        int dlo = qw0 - (kj0 + 31);
-        dlo = dlo < 1 - a.lmax ? 1 - a.lmax : (dlo > a.lmax - 1 ? a.lmax - 1 : dlo);
-        mlo = sBucket[dlo + a.lmax - 1];
+        const int dlo = qw0 - (kj0 + 31);
         float *c2pw = sRel + (w * 2) * 32 * RP;
         float *p2cw = c2pw + 32 * RP;
         const int64_t hd = (int64_t)H * D;
-        const int prow = mlo + (lane & 31);
         const T *krow = &sK[(kt * 32 + (lane & 31)) * LDK + g * MF::KLANE];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++) {
-          const int pr = prow + mt * 32 < a.nb ? prow + mt * 32 : a.nb - 1;
+          int di = dlo + (lane & 31) + mt * 32 + a.lmax - 1;  // this lane's distance row
+          di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
+          const int pr = sBucket[di];  // < nb: the relidx table is checked against the tables
           const T *pk = (const T *)a.pos_key + pr * hd + h * D + g * MF::KLANE;
           const T *pq = (const T *)a.pos_query + pr * hd + h * D + g * MF::KLANE;
           float16v cq = {}, ck = {};
@@ -209,7 +209,7 @@ attn_kernel(AttnArgs a, Packing p) {
             cq = MF::mma(fk, qf[s], cq);  // [m][query]: lane = query
             ck = MF::mma(fq, kf, ck);     // [m][key]: lane = key
           }
-          // registers 4 r4 .. 4 r4 + 3 are buckets mlo + 32 mt + 8 r4 + 4 g + {0..3}
+          // registers 4 r4 .. 4 r4 + 3 are distance rows 32 mt + 8 r4 + 4 g + {0..3}
 #pragma unroll
           for (int r4 = 0; r4 < 4; r4++) {
             const int mm = mt * 32 + 8 * r4 + 4 * g;
@@ -219,8 +219,11 @@ attn_kernel(AttnArgs a, Packing p) {
                 float4v{ck[4 * r4], ck[4 * r4 + 1], ck[4 * r4 + 2], ck[4 * r4 + 3]};
           }
         }
-        c2pW = c2pw + (lane & 31) * RP - mlo;  // this lane's query row, indexed by bucket
-        p2cW = p2cw - mlo;
+        // score (query q, key jl) is at distance row q + 31 - jl: c2p[q][q + 31 - jl] and
+        // p2c[jl][q + 31 - jl]. With jl = jc + 4 g (jc a constant per register) the lane's part
+        // goes into the bases and each read has a constant, non-negative offset.
+        c2pW = c2pw + (lane & 31) * (RP + 1) - 4 * g;
+        p2cW = p2cw + (lane & 31) + 31 + 4 * g * (RP - 1);
       }
       const int k0 = kb + kt * 32;
       auto scores = [&](auto masked_t) {
@@ -232,14 +235,10 @@ attn_kernel(AttnArgs a, Packing p) {
           const int jl = 8 * (r >> 2) + 4 * g + (r & 3);
           float v = sc[kt][r];
           if constexpr (REL) {
-            // gathered unconditionally (no branch per score): indices clamped into the tables,
-            // the masked pairs' values are discarded below
-            int di = qi - (k0 + jl) + a.lmax - 1;
-            di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
-            int mm = sBucket[di] - mlo;
-            mm = mm < 0 ? 0 : (mm > 63 ? 63 : mm);
-            v = v + c2pW[mlo + mm];
-            v = v + p2cW[jl * RP + mlo + mm];
+            // read unconditionally (no branch per score); masked pairs are discarded below
+            const int jc = 8 * (r >> 2) + (r & 3);
+            v = v + c2pW[31 - jc];
+            v = v + p2cW[jc * (RP - 1)];
           }
           if constexpr (MASKED) {
             bool ok = jl < lim;
