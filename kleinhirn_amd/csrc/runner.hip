@@ -797,6 +797,23 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
       break;
     }
     case S_LN: {
+      if (pl->by_ids && s.in[0].id == pl->in_emb) {
+        // the embedding LN of plans without position or type tables (DeBERTa, ModernBERT) over
+        // rows gathered from the device word table: the embln kernel with no added tables
+        EmbLnArgs a;
+        a.table = pl->ctx->words->p;
+        a.ids = (const int32_t *)pl->d_ids.p;
+        a.gamma = bufp(pl, s.in[2]);
+        a.beta = bufp(pl, s.in[3]);
+        a.out = bufp(pl, s.in[5]);
+        a.N = s.N;
+        a.posids = 1;  // no position rows: the (absent) type words are not read
+        a.eps = s.eps;
+        begin("embln", 8.0 * pl->T * s.N, 2.0 * es * pl->T * s.N + 4.0 * pl->T);
+        embln(f16, a, pk, st);
+        end();
+        break;
+      }
       const void *b = s.mode == 2 ? bufp(pl, s.in[1]) : nullptr;
       begin("layernorm", 8.0 * rows * s.N, (double)es * ((s.mode == 2 ? 3.0 : 2.0) * rows * s.N + 2.0 * s.N));
       layernorm(f16, bufp(pl, s.in[0]), b, bufp(pl, s.in[2]), bufp(pl, s.in[3]), bufp(pl, s.in[5]), rows, s.N, s.eps,
@@ -1061,6 +1078,37 @@ static void run_steps(kh_plan *pl, const LaunchHook &hook) {
 
 // ---- the twin: the second half of a small batch on its own stream ------------------------------
 
+static void init_buffer(kh_plan *plan, const char *id, const void *data, size_t bytes) {
+  auto it = plan->bufs.find(id);
+  if (it == plan->bufs.end()) fail(KH_EINVAL, std::string("plan buffer ") + id + " missing");
+  Buffer &b = it->second;
+  if ((int64_t)bytes > b.bytes) fail(KH_EINVAL, std::string("init of ") + id + " larger than the buffer");
+  b.init.assign((const uint8_t *)data, (const uint8_t *)data + bytes);
+  const std::string sid = id;
+  if (sid == "relidx") {
+    // relidx[i][j] depends on i - j only: keep bucket(i - j) for i - j in [-(L-1), L-1]
+    const int L = plan->L;
+    if (bytes != (size_t)L * L * 4) fail(KH_EINVAL, "relidx must hold L * L u32");
+    const uint32_t *t = (const uint32_t *)data;
+    plan->bucket_host.assign(2 * L - 1, 0);
+    for (int d = -(L - 1); d <= L - 1; d++) plan->bucket_host[d + L - 1] = (int32_t)(d >= 0 ? t[(size_t)d * L] : t[-d]);
+    for (int i = 0; i < L; i++)
+      for (int j = 0; j < L; j++)
+        if ((int32_t)t[(size_t)i * L + j] != plan->bucket_host[i - j + L - 1])
+          fail(KH_EUNSUPPORTED, "relidx is not a function of i - j");
+    for (int32_t v : plan->bucket_host)
+      if (v < 0 || v >= plan->rel_nb) fail(KH_EINVAL, "relidx entry outside the position table");
+    plan->d_bucket.alloc(plan->bucket_host.size() * 4);
+    KH_CHECK(hipMemcpy(plan->d_bucket.p, plan->bucket_host.data(), plan->bucket_host.size() * 4, hipMemcpyHostToDevice));
+    return;
+  }
+  if (b.mem) KH_CHECK(hipMemcpy(b.mem->p, data, bytes, hipMemcpyHostToDevice));
+  if (sid == plan->prune_markers) {
+    memcpy(plan->markers_shadow.data(), data, bytes);
+    check_markers(plan);
+  }
+}
+
 static int64_t env_int(const char *name, int64_t dflt) {
   const char *e = getenv(name);
   return e && *e ? atoll(e) : dflt;
@@ -1083,7 +1131,7 @@ static int choose_split(const kh_plan *pl, int rows) {
     pre[b + 1] = pre[b] + len;
   }
   const int64_t T = pre[pl->B];
-  if (T < 2048 || T >= env_int("KH_SPLIT_T", 65536)) return 0;
+  if (T < env_int("KH_SPLIT_MIN", 2048) || T >= env_int("KH_SPLIT_T", 65536)) return 0;
   int split = 1;
   while (split < pl->B - 1 && 2 * pre[split] < T) split++;
   if (pre[split] == 0 || pre[split] == T) return 0;
@@ -1108,9 +1156,30 @@ static void ensure_twin(kh_plan *pl) {
   pl->twin = t;
 }
 
+// bytes per sequence of a per-sequence init table (the gather markers: K triples of u32 per
+// sequence, the row first); 0 for tables that do not index sequences
+static size_t seq_stride(const kh_plan *pl, const std::string &id) {
+  for (const Step &s : pl->steps)
+    if (s.kind == S_GATHER && s.markers_id == id) return (size_t)s.Kmk * 3 * 4;
+  return 0;
+}
+
+// a per-sequence init table as the twin holds it: sequence split + j at slot j, zeros after
+static std::vector<uint8_t> shifted_table(const std::vector<uint8_t> &v, size_t per, int split) {
+  std::vector<uint8_t> out(v.size(), 0);
+  const size_t from = (size_t)split * per;
+  if (from < v.size()) memcpy(out.data(), v.data() + from, v.size() - from);
+  return out;
+}
+
 // the twin's host arrays: sequences [split, B) of this plan's upload at slots [0, B - split)
 static void stage_twin(kh_plan *pl, int split) {
   kh_plan *t = pl->twin;
+  for (const auto &in : pl->init_log)
+    if (const size_t per = seq_stride(pl, in.first)) {
+      const std::vector<uint8_t> v = shifted_table(in.second, per, split);
+      init_buffer(t, in.first.c_str(), v.data(), v.size());
+    }
   const size_t L = pl->L, M = L * pl->B, moved = (size_t)(pl->B - split) * L, from = (size_t)split * L;
   t->mask_host.assign(M, 0.f);
   memcpy(t->mask_host.data(), pl->mask_host.data() + from, moved * 4);
@@ -1124,10 +1193,17 @@ static void stage_twin(kh_plan *pl, int split) {
     t->ids_host.assign(M, 0);
     memcpy(t->ids_host.data(), pl->ids_host.data() + from, moved * 4);
   } else {
+    // only the valid rows of each moved sequence (pack reads no others): about T / 2 rows
     const size_t row = (size_t)pl->E * (pl->f16 ? 2 : 4);
-    t->emb_host.assign(M * row, 0);
-    if (pl->emb_host.size() > from * row)
-      memcpy(t->emb_host.data(), pl->emb_host.data() + from * row, std::min(moved * row, pl->emb_host.size() - from * row));
+    if (t->emb_host.size() != M * row) t->emb_host.resize(M * row);
+    for (int b = split; b < pl->B; b++) {
+      const float *m = pl->mask_host.data() + (size_t)b * L;
+      size_t len = 0;
+      while (len < L && m[len] > 0.5f) len++;
+      const size_t src = (size_t)b * L * row, dst = (size_t)(b - split) * L * row;
+      if (src + len * row > pl->emb_host.size()) fail(KH_EINVAL, "word rows shorter than the mask's valid rows");
+      if (len) memcpy(t->emb_host.data() + dst, pl->emb_host.data() + src, len * row);
+    }
   }
   t->uploaded = true;
   t->dirty = true;
@@ -1136,7 +1212,8 @@ static void stage_twin(kh_plan *pl, int split) {
 // packs (when the upload or the split changed) and enqueues the forward of the whole batch
 static void launch_forward(kh_plan *pl, int rows, const LaunchHook &hook, bool sequential) {
   // the split depends on the upload (dirty), the row count and the two switches
-  const int64_t env = env_int("KH_NO_SPLIT", 0) * 1000003 + env_int("KH_SPLIT_T", 65536);
+  const int64_t env =
+      (env_int("KH_NO_SPLIT", 0) * 1000003 + env_int("KH_SPLIT_T", 65536)) * 1000003 + env_int("KH_SPLIT_MIN", 2048);
   if (pl->dirty || pl->split_memo < 0 || rows != pl->split_memo_rows || env != pl->split_memo_env) {
     pl->split_memo = choose_split(pl, rows);
     pl->split_memo_rows = rows;
@@ -1636,36 +1713,6 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
   KH_API_END
 }
 
-static void init_buffer(kh_plan *plan, const char *id, const void *data, size_t bytes) {
-  auto it = plan->bufs.find(id);
-  if (it == plan->bufs.end()) fail(KH_EINVAL, std::string("plan buffer ") + id + " missing");
-  Buffer &b = it->second;
-  if ((int64_t)bytes > b.bytes) fail(KH_EINVAL, std::string("init of ") + id + " larger than the buffer");
-  b.init.assign((const uint8_t *)data, (const uint8_t *)data + bytes);
-  const std::string sid = id;
-  if (sid == "relidx") {
-    // relidx[i][j] depends on i - j only: keep bucket(i - j) for i - j in [-(L-1), L-1]
-    const int L = plan->L;
-    if (bytes != (size_t)L * L * 4) fail(KH_EINVAL, "relidx must hold L * L u32");
-    const uint32_t *t = (const uint32_t *)data;
-    plan->bucket_host.assign(2 * L - 1, 0);
-    for (int d = -(L - 1); d <= L - 1; d++) plan->bucket_host[d + L - 1] = (int32_t)(d >= 0 ? t[(size_t)d * L] : t[-d]);
-    for (int i = 0; i < L; i++)
-      for (int j = 0; j < L; j++)
-        if ((int32_t)t[(size_t)i * L + j] != plan->bucket_host[i - j + L - 1])
-          fail(KH_EUNSUPPORTED, "relidx is not a function of i - j");
-    for (int32_t v : plan->bucket_host)
-      if (v < 0 || v >= plan->rel_nb) fail(KH_EINVAL, "relidx entry outside the position table");
-    plan->d_bucket.alloc(plan->bucket_host.size() * 4);
-    KH_CHECK(hipMemcpy(plan->d_bucket.p, plan->bucket_host.data(), plan->bucket_host.size() * 4, hipMemcpyHostToDevice));
-    return;
-  }
-  if (b.mem) KH_CHECK(hipMemcpy(b.mem->p, data, bytes, hipMemcpyHostToDevice));
-  if (sid == plan->prune_markers) {
-    memcpy(plan->markers_shadow.data(), data, bytes);
-    check_markers(plan);
-  }
-}
 
 
 int kh_plan_init_buffer(kh_plan *plan, const char *id, const void *data, size_t bytes) {
@@ -1682,7 +1729,17 @@ int kh_plan_init_buffer(kh_plan *plan, const char *id, const void *data, size_t 
       logged = true;
     }
   if (!logged) plan->init_log.push_back({id, copy});
-  if (plan->twin) init_buffer(plan->twin, id, data, bytes);
+  if (plan->twin) {
+    // per-sequence tables move with the twin's sequences (stage_twin shifts them again when the
+    // split changes)
+    const size_t per = seq_stride(plan, id);
+    if (per && plan->split > 0) {
+      const std::vector<uint8_t> v = shifted_table(copy, per, plan->split);
+      init_buffer(plan->twin, id, v.data(), v.size());
+    } else {
+      init_buffer(plan->twin, id, data, bytes);
+    }
+  }
   KH_API_END
 }
 
@@ -1751,6 +1808,12 @@ int kh_upload_ids(kh_plan *plan, const int32_t *ids, size_t id_count, const floa
     fail(KH_EINVAL, "word table dtype or width differs from the plan");
   const size_t M = (size_t)plan->L * plan->B;
   if (!ids || id_count > M) fail(KH_EINVAL, "ids must hold up to L * B values");
+  // the word rows feed the embedding LN only (embln, or a layernorm without residual): the run
+  // gathers them from the table inside that step
+  for (const Step &s : plan->steps)
+    for (int i = 0; i < 6; i++)
+      if (s.in[i].id == plan->in_emb && !(i == 0 && (s.kind == S_EMBLN || (s.kind == S_LN && s.mode != 2))))
+        fail(KH_EUNSUPPORTED, "op " + s.name + " reads the word rows: upload them (kh_upload)");
   stage_common(plan, mask, mask_count, type_ids, type_count);
   plan->ids_host.assign(M, 0);
   memcpy(plan->ids_host.data(), ids, id_count * 4);

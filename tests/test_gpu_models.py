@@ -102,6 +102,23 @@ def test_device_word_gather_equals_host_gather():
     assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("key", ["c3b", "c4"])
+def test_device_ids_without_position_tables(key):
+    """Plans whose embedding is a plain layernorm of the word rows (DeBERTa, ModernBERT) gather the
+    rows from the device word table inside that layernorm; the ids path meets the oracle's bars and
+    stays within f16 rounding of the host-rows path."""
+    case, ref = case_and_oracle(key)
+    rows = hip_outputs(case, f16=True)
+    ids = hip_outputs(case, f16=True, by_ids=True)
+    if key == "c4":
+        assert cosine_rows(ref, ids).min() >= 0.999
+        assert cosine_rows(rows, ids).min() >= 0.9999
+    else:
+        d = decision_parity(ref, ids)
+        assert d["mismatched"] == 0 and d["delta"] <= 2e-2, d
+        assert np.abs(rows - ids).max() <= 2e-2
+
+
 def test_fused_product_steps_match_separate_ops(monkeypatch):
     """ModernBERT: GEMM + GeGLU, GEMM + RoPE and GEMM + residual add run fused in the product's
     epilogue; with fusion off (KH_NO_FUSION) the separate kernels run. Both apply the same f32
@@ -200,3 +217,49 @@ def test_read_scores_equals_scores_of_the_output(key):
         assert cosine_rows(want, s).min() >= 0.999
     r.destroy()
     be.dispose()
+
+
+TOKEN_HEAD = {"type": "token", "steps": [{"op": "dense", "name": "head.tok", "in": 768, "out": 5, "act": "none",
+                                          "bias": True}]}
+
+
+def token_case():
+    """A token-classification head (one dense step per row, src/plan/build.ts token branch) on two
+    RoBERTa-base layers and six ragged c2 sequences."""
+    from tests.helpers import Case
+    c = workload_case("c2", 6, 2, 512)
+    return Case(c.spec, TOKEN_HEAD, c.ids, c.length)
+
+
+def token_oracle(case) -> list:
+    """The oracle's rows of each sequence (a B = 1 plan per sequence), [len, classes] each."""
+    from oracle.oracle import OracleRuntime
+    plan = build_plan(case.spec, case.head, case.length, 1, False)
+    p = OracleRuntime(case.weights, [plan]).plan(plan, threads=8)
+    table = case.weights["embeddings.word.weight"]
+    outs = []
+    for seq in case.ids:
+        ri = inputs.run_input(case.spec, table, [seq], case.length)
+        p.upload(ri["embeddings"], ri["mask"], ri["typeIds"])
+        p.run(len(seq))
+        outs.append(p.read_output().reshape(case.length, -1)[:len(seq)])
+    return outs
+
+
+@pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
+def test_token_head_matches_oracle(f16):
+    """Per-token logits of the token head: row i of sequence b at b * L + i, zeros past each
+    sequence; f32 within 1e-3 with identical argmax, f16 with identical decisions outside close calls."""
+    case = token_case()
+    ref = token_oracle(case)
+    got = hip_outputs(case, f16).reshape(len(case.ids), case.length, -1)
+    for b, r in enumerate(ref):
+        n = len(r)
+        assert not got[b, n:].any(), f"sequence {b}: rows past the sequence are not zero"
+        if f16:
+            d = decision_parity(r, got[b, :n])
+            assert d["mismatched"] == 0, (b, d)
+            assert cosine_rows(r, got[b, :n]).min() >= 0.999
+        else:
+            assert np.abs(r - got[b, :n]).max() <= 1e-3, (b, np.abs(r - got[b, :n]).max())
+            assert np.array_equal(r.argmax(1), got[b, :n].argmax(1))
