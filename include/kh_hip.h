@@ -196,6 +196,14 @@ int kh_upload(kh_plan *plan, const void *emb, size_t emb_bytes, const float *mas
 int kh_upload_ids(kh_plan *plan, const int32_t *ids, size_t id_count, const float *mask,
                   size_t mask_count, const uint32_t *type_ids, size_t type_count);
 
+/* The packedMarkers part of PlanRunner.upload (RunInput.packedMarkers, src/plan/executor.ts:28,
+ * 385-388) for plans with a markers input (GLiNER2 span heads): per sequence 3 * markers u32, the
+ * marker row indices, the marker mask as f32 bits and the group ids; count must be
+ * 3 * markers * batch. Every row index must be below the plan length (KH_EINVAL at kh_run). Kept
+ * until replaced; before the first call every slot is masked. A marker whose row lies past its
+ * sequence's valid rows gathers a zero state (the reference reads the padding row's state). */
+int kh_upload_markers(kh_plan *plan, const uint32_t *packed, size_t count);
+
 /* PlanRunner.run (src/plan/executor.ts:295-297): one forward over `rows` rows (the real rows of
  * a B = 1 call, L * B for a batch plan), enqueued on the plan's stream; returns without waiting.
  * A batch call with fewer than KH_SPLIT_T (environment, default 65536) valid rows runs as two
@@ -203,7 +211,8 @@ int kh_upload_ids(kh_plan *plan, const int32_t *ids, size_t id_count, const floa
 int kh_run(kh_plan *plan, int32_t rows);
 
 /* PlanRunner.readOutput (src/plan/executor.ts:398-408): waits, then writes rows * cols f32
- * values (f16 storage converted) in the plan's output layout. */
+ * values (f16 storage converted; f32 output buffers, as a GLiNER2 plan's logits, as they are) in
+ * the plan's output layout. */
 int kh_read_output(kh_plan *plan, float *out, size_t count);
 
 /* Waits for the plan's stream. */

@@ -87,6 +87,11 @@ struct EmbLnArgs {
 };
 void embln(bool f16, const EmbLnArgs &a, const Packing &p, hipStream_t s);
 
+// GLiNER2 logits: logits[k] = raw[k] / temp where marker k's mask word (f32 bits at
+// b * 3K + K + k mod K of the packed payloads, b = k / K) exceeds 0.5, else -1e4; total = B * K.
+void mask_logits(bool f16, const void *raw, const uint32_t *packed, float *logits, int K, float temp, int64_t total,
+                 hipStream_t s);
+
 // LN over rows: MODE 2 adds b first. rows = T (packed) or B (sequence rows).
 void layernorm(bool f16, const void *a, const void *b, const void *gamma, const void *beta, void *out,
                int64_t rows, int N, float eps, hipStream_t s);

@@ -494,6 +494,27 @@ void gather_rows(bool f16, const void *x, const uint32_t *markers, void *states,
                        (float *)states, K, D, p.B, p.cu);
 }
 
+// one thread per marker (src/kernels/masklogits.wgsl; src/wasm/plan.ts:545-551)
+template <typename T>
+__global__ void __launch_bounds__(256) mask_logits_kernel(const T *__restrict__ raw, const uint32_t *__restrict__ packed,
+                                                          float *__restrict__ logits, int K, float temp, int64_t total) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= total) return;
+  const int64_t b = k / K;
+  const float m = __uint_as_float(packed[b * 3 * K + K + (k - b * K)]);
+  logits[k] = m > 0.5f ? (float)raw[k] / temp : -1e4f;
+}
+
+void mask_logits(bool f16, const void *raw, const uint32_t *packed, float *logits, int K, float temp, int64_t total,
+                 hipStream_t s) {
+  if (total <= 0) return;
+  const dim3 grid((unsigned)((total + 255) / 256));
+  if (f16)
+    launch((mask_logits_kernel<half_t>), grid, dim3(256), 0, s, (const half_t *)raw, packed, logits, K, temp, total);
+  else
+    launch((mask_logits_kernel<float>), grid, dim3(256), 0, s, (const float *)raw, packed, logits, K, temp, total);
+}
+
 void to_f32(bool f16, const void *src, float *dst, int64_t n, hipStream_t s) {
   if (n <= 0) return;
   if (f16)

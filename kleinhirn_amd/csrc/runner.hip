@@ -123,7 +123,7 @@ struct kh_ctx {
 
 namespace kh {
 
-enum StepKind { S_EMBLN, S_LN, S_GEMM, S_ADD, S_GEGLU, S_ROPE, S_ATTN, S_POOL, S_GATHER, S_COMPACT };
+enum StepKind { S_EMBLN, S_LN, S_GEMM, S_ADD, S_GEGLU, S_ROPE, S_ATTN, S_POOL, S_GATHER, S_COMPACT, S_MASKL };
 
 // A buffer reference of a step: device pointer resolved at plan creation.
 struct Ref {
@@ -182,6 +182,10 @@ struct kh_plan {
   std::vector<uint8_t> markers_shadow;  // host copy of that markers buffer
   bool markers_first = true;
   std::string in_emb, in_mask, in_tt;
+  std::string in_markers;             // packed marker payloads (GLiNER2 span heads), or empty
+  std::vector<uint32_t> markers_host;  // the last kh_upload_markers payload
+  bool markers_dirty = false;
+  bool out_f32 = false;                // output buffer holds f32 whatever the storage dtype
   std::string out_buf;
   int out_rows = 0, out_cols = 0;
   bool out_packed = false;
@@ -413,6 +417,14 @@ static std::vector<Step> lower(const Parsed &pp, bool f16, int L, std::vector<st
         s.N = cint(op, "N");
         s.mode = cint(op, "MODE");
         s.seq_rows = true;
+      } else if (kn == "masklogits") {
+        // raw, packed markers, f32 logits (src/plan/build.ts:371-375)
+        s.kind = S_MASKL;
+        for (int b = 0; b < 3; b++) s.in[b].id = bind(op, b);
+        s.Kmk = cint(op, "K");
+        s.scale = (float)cnum(op, "TEMP");
+        s.seq_rows = true;
+        if (s.Kmk < 1) fail(KH_EINVAL, "masklogits K must be positive");
       } else if (kn == "gather") {
         s.kind = S_GATHER;
         s.markers_id = bind(op, 0);
@@ -639,7 +651,8 @@ static void prune_tail(kh_plan *pl) {
       g = i;
     }
   }
-  if (g < 0 || st[g].kind != S_GATHER || st[g].Kmk != 1) return;
+  // (marker heads gather rows their uploaded payload names: no tail on row 0)
+  if (g < 0 || st[g].kind != S_GATHER || st[g].Kmk != 1 || !pl->in_markers.empty()) return;
   for (int i = 0; i < g; i++)
     if (st[i].kind == S_ATTN) a = i;
   if (a < 0) return;
@@ -870,6 +883,14 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
       pool(f16, bufp(pl, s.in[0]), bufp(pl, s.in[1]), s.N, s.mode, pk, st);
       end();
       break;
+    case S_MASKL: {
+      const int64_t total = (int64_t)pl->B * s.Kmk;
+      begin("masklogits", (double)total, (double)total * (es + 4.0 + 4.0));
+      mask_logits(f16, bufp(pl, s.in[0]), (const uint32_t *)bufp(pl, s.in[1]), (float *)bufp(pl, s.in[2]), s.Kmk,
+                  s.scale, total, st);
+      end();
+      break;
+    }
     case S_GATHER: {
       auto it = pl->bufs.find(s.markers_id);
       const uint32_t *mk = it != pl->bufs.end() && it->second.mem ? (const uint32_t *)it->second.mem->p : nullptr;
@@ -996,10 +1017,11 @@ static void pack(kh_plan *pl, int rows, int b_end) {
   if (pl->d_tiles_first.bytes < tiles_first.size() * sizeof(int2) || !pl->d_tiles_first.p)
     pl->d_tiles_first.alloc(tiles_first.size() * sizeof(int2));
   KH_CHECK(hipStreamSynchronize(pl->stream));  // staging may still feed an earlier copy
-  // seven blocks at most (cu, row_pos, row_seq, tiles, first tiles, type ids, ids), each 16-byte aligned
+  // eight blocks at most (cu, row_pos, row_seq, tiles, first tiles, type ids, ids, markers), each
+  // 16-byte aligned
   const size_t T1 = (size_t)std::max<int64_t>(T, 1);
-  const size_t meta =
-      (size_t)(B + 1) * 4 + 4 * T1 * 4 + (tiles.size() + tiles_first.size()) * sizeof(int2) + 7 * 16;
+  const size_t meta = (size_t)(B + 1) * 4 + 4 * T1 * 4 + (tiles.size() + tiles_first.size()) * sizeof(int2) +
+                      pl->markers_host.size() * 4 + 8 * 16;
   pl->pin_meta.ensure(meta);
   char *mp = (char *)pl->pin_meta.p;
   char *const mend = mp + meta;
@@ -1033,6 +1055,18 @@ static void pack(kh_plan *pl, int rows, int b_end) {
       }
     if (pl->d_tt.bytes < tt.size() * 4 || !pl->d_tt.p) pl->d_tt.alloc(tt.size() * 4);
     put(pl->d_tt, tt.data(), tt.size() * 4);
+  }
+  // packed marker payloads: B blocks of 3 K u32 (row indices, mask bits, groups), rows within L
+  if (!pl->in_markers.empty()) {
+    const int K = pl->markers;
+    for (int b = 0; b < B; b++)
+      for (int k = 0; k < K; k++) {
+        const uint32_t r = pl->markers_host[(size_t)b * 3 * K + k];
+        if (r >= (uint32_t)L)
+          fail(KH_EINVAL, "marker " + std::to_string(k) + " of sequence " + std::to_string(b) + " names row " +
+                              std::to_string(r) + ", the plan length is " + std::to_string(L));
+      }
+    put(*pl->bufs.at(pl->in_markers).mem, pl->markers_host.data(), pl->markers_host.size() * 4);
   }
   // packed word rows or ids
   if (pl->by_ids) {
@@ -1120,6 +1154,7 @@ static int64_t env_int(const char *name, int64_t dflt) {
 // about half the rows.
 static int choose_split(const kh_plan *pl, int rows) {
   if (pl->is_twin || pl->B < 2 || rows != pl->L * pl->B || env_int("KH_NO_SPLIT", 0)) return 0;
+  if (!pl->in_markers.empty()) return 0;  // marker heads run whole
   const bool per_seq = !pl->out_packed && pl->out_rows == pl->B;
   const bool per_tok = pl->out_packed && pl->out_rows == pl->L * pl->B;
   if (!per_seq && !per_tok) return 0;
@@ -1583,7 +1618,6 @@ int kh_plan_check(kh_ctx *ctx, const char *plan_json, size_t len) {
   if (ctx) check_bindings(ctx, pp, steps, f16, errors);
   if (pp.root.has("rowSelect") && pp.root.at("rowSelect").kind != Json::Null)
     errors.push_back("rowSelect (Julia type rows) is outside the encoder heads");
-  if (pp.root.at("inputs").has("markers")) errors.push_back("marker inputs (GLiNER, Julia) are outside the encoder heads");
   if (!errors.empty()) fail(KH_EUNSUPPORTED, join_errors(errors));
   KH_API_END
 }
@@ -1606,8 +1640,11 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
   pl->steps = lower(pp, pl->f16, pl->L, errors);
   check_bindings(ctx, pp, pl->steps, pl->f16, errors);
   const Json &inputs = pp.root.at("inputs");
-  if (inputs.has("markers")) errors.push_back("marker inputs (GLiNER, Julia) are outside the encoder heads");
   if (!errors.empty()) fail(KH_EUNSUPPORTED, join_errors(errors));
+  if (inputs.has("markers")) {
+    pl->in_markers = inputs.at("markers").str();
+    if (pl->markers < 1) fail(KH_EINVAL, "a plan with a markers input needs markers >= 1");
+  }
   pl->in_emb = inputs.at("embeddings").str();
   pl->out_buf = pp.root.at("output").at("buffer").str();
   if (!getenv("KH_NO_FUSION")) fuse_steps(pl.get());
@@ -1617,13 +1654,21 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
   pl->out_buf = o.at("buffer").str();
   pl->out_rows = (int)o.at("rows").integer();
   pl->out_cols = (int)o.at("cols").integer();
-  if (o.at("dtype").str() != "storage") fail(KH_EUNSUPPORTED, "output dtype " + o.at("dtype").str());
+  const std::string odt = o.at("dtype").str();
+  if (odt != "storage" && odt != "f32") fail(KH_EUNSUPPORTED, "output dtype " + odt);
+  pl->out_f32 = odt == "f32" || !pl->f16;
 
   for (const Json &b : pp.root.at("buffers").arr()) {
     Buffer buf;
     buf.bytes = b.at("bytes").integer();
     buf.usage = b.at("usage").str();
     pl->bufs.emplace(b.at("id").str(), std::move(buf));
+  }
+  if (!pl->in_markers.empty()) {
+    // payloads start as masked slots at row 0 (logits -1e4) until kh_upload_markers
+    pl->markers_host.assign((size_t)3 * pl->markers * pl->B, 0u);
+    if (!pl->bufs.count(pl->in_markers) || pl->bufs.at(pl->in_markers).bytes < (int64_t)pl->markers_host.size() * 4)
+      fail(KH_EINVAL, "markers buffer smaller than 3 * markers * batch u32");
   }
   if (!getenv("KH_NO_PRUNE")) prune_tail(pl.get());
   // row spaces and uses
@@ -1648,6 +1693,7 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
       case S_POOL: dst = &s.in[1].id; break;
       case S_GATHER: dst = &s.in[1].id; break;
       case S_COMPACT: dst = &s.in[1].id; break;
+      case S_MASKL: dst = &s.in[2].id; break;
       default: break;
     }
     if (dst) {
@@ -1821,6 +1867,20 @@ int kh_upload_ids(kh_plan *plan, const int32_t *ids, size_t id_count, const floa
   KH_API_END
 }
 
+int kh_upload_markers(kh_plan *plan, const uint32_t *packed, size_t count) {
+  KH_API_BEGIN
+  if (!plan) fail(KH_EINVAL, "null plan");
+  require_live(plan->ctx);
+  if (plan->in_markers.empty()) fail(KH_EINVAL, "the plan has no markers input");
+  const size_t want = (size_t)3 * plan->markers * plan->B;
+  if (!packed || count != want)
+    fail(KH_EINVAL, "packed markers hold " + std::to_string(count) + " u32, the plan takes 3 * " +
+                        std::to_string(plan->markers) + " * " + std::to_string(plan->B) + " = " + std::to_string(want));
+  memcpy(plan->markers_host.data(), packed, want * 4);
+  plan->dirty = true;  // the payload travels with the next run's packed metadata
+  KH_API_END
+}
+
 int kh_run(kh_plan *plan, int32_t rows) {
   KH_API_BEGIN
   if (!plan) fail(KH_EINVAL, "null plan");
@@ -1879,12 +1939,13 @@ static void read_into(kh_plan *plan, float *out, size_t n) {
   const size_t es = plan->f16 ? 2 : 4;
   const int cols = plan->out_cols;
   if (!plan->out_packed) {
-    std::vector<uint8_t> raw(n * es);
-    KH_CHECK(hipMemcpyAsync(raw.data(), b.mem->p, n * es, hipMemcpyDeviceToHost, plan->stream));
+    const size_t oes = plan->out_f32 ? 4 : es;
+    std::vector<uint8_t> raw(n * oes);
+    KH_CHECK(hipMemcpyAsync(raw.data(), b.mem->p, n * oes, hipMemcpyDeviceToHost, plan->stream));
     KH_CHECK(hipStreamSynchronize(plan->stream));
     // sequences without a valid row: zero output (the reference computes them from padding)
-    for (size_t i = 0; i < n; i++) out[i] = plan->f16 ? (float)((const _Float16 *)raw.data())[i] : ((const float *)raw.data())[i];
-    if (plan->out_rows == plan->B)
+    for (size_t i = 0; i < n; i++) out[i] = plan->out_f32 ? ((const float *)raw.data())[i] : (float)((const _Float16 *)raw.data())[i];
+    if (plan->out_rows == plan->B && plan->in_markers.empty())
       for (int bb = 0; bb < plan->B; bb++)
         if (plan->cu[bb + 1] == plan->cu[bb]) memset(out + (size_t)bb * cols, 0, (size_t)cols * 4);
   } else {

@@ -25,7 +25,8 @@ def export_case(dirname: str, plan: dict, weights: dict | None = None, run_input
         json.dump(plan_json(plan), f)
     meta = {"checkOnly": check_only, "weights": [], "inits": {}, "rows": rows or 0,
             "typeIds": bool(run_input is not None and run_input.get("typeIds") is not None),
-            "manifest": manifest, "manifestFlags": manifest_flags, "ids": ids is not None}
+            "manifest": manifest, "manifestFlags": manifest_flags, "ids": ids is not None,
+            "markers": bool(run_input is not None and run_input.get("packedMarkers") is not None)}
     if ids is not None:
         np.ascontiguousarray(ids, dtype=np.int32).tofile(os.path.join(dirname, "ids.bin"))
     if not check_only:
@@ -45,6 +46,8 @@ def export_case(dirname: str, plan: dict, weights: dict | None = None, run_input
         np.ascontiguousarray(run_input["mask"], dtype=np.float32).tofile(os.path.join(dirname, "mask.bin"))
         if meta["typeIds"]:
             np.ascontiguousarray(run_input["typeIds"], dtype=np.uint32).tofile(os.path.join(dirname, "tt.bin"))
+        if meta["markers"]:
+            np.ascontiguousarray(run_input["packedMarkers"], dtype=np.uint32).tofile(os.path.join(dirname, "mk.bin"))
     with open(os.path.join(dirname, "meta.json"), "w") as f:
         json.dump(meta, f)
 

@@ -96,10 +96,17 @@ def _elements_written(op: dict) -> int:
     return 0
 
 
-def build_plan(spec: dict, head: dict, length: int, batch: int, f16: bool) -> dict:
-    """src/plan/build.ts:109-526 for classify, token and embed heads."""
-    if head["type"] not in ("classify", "token", "embed"):
+def build_plan(spec: dict, head: dict, length: int, batch: int, f16: bool, markers: int | None = None) -> dict:
+    """src/plan/build.ts:109-526 for classify, token, embed and GLiNER2 heads. `markers` is the
+    reference's BuildOptions.markers (marker slots per sequence of a GLiNER2 plan; the head's own
+    count when None)."""
+    if head["type"] not in ("classify", "token", "embed", "gliner2"):
         raise ValueError(f"head {head['type']} is not an encoder head of this runner")
+    pooled = head["type"] != "gliner2"
+    markers = 0 if pooled else int(head["markers"] if markers is None else markers)
+    if not pooled and markers < 1:
+        raise ValueError("a GLiNER2 plan needs at least one marker slot")
+    K = markers * batch
     names = tensor_names_for(spec)
     H = spec["hidden"]
     E = spec["embeddingSize"]
@@ -181,6 +188,9 @@ def build_plan(spec: dict, head: dict, length: int, batch: int, f16: bool) -> di
             ln("final", 0, ["x", "dummy", f"w:{names.finalNormW}",
                             f"w:{names.finalNormB}" if names.finalNormB else "zero", "mask", "tmp"])]})
         stream = "tmp"
+
+    if not pooled:
+        return _gliner2_plan(spec, head, segments, stream, length, batch, f16, markers, K, bytes_of, mm, absolute)
 
     # Head (src/plan/build.ts:296-357)
     head_buffers = []
@@ -306,6 +316,110 @@ def build_plan(spec: dict, head: dict, length: int, batch: int, f16: bool) -> di
     }
 
 
+def _gliner2_plan(spec, head, segments, stream, length, batch, f16, markers, K, bytes_of, mm, absolute) -> dict:
+    """The GLiNER2 span head (src/plan/build.ts:358-377): the hidden states at the K = markers x
+    batch marker rows (gather over the packed markers input: per sequence K indices, K mask words
+    as f32 bits, K group ids), fc1 with ReLU, fc2 to one raw logit per marker, and masklogits
+    (raw / temperature where the marker's mask is set, else -1e4) into an f32 output. Buffers as
+    src/plan/build.ts:432-526 lays them out for a marker head."""
+    H = spec["hidden"]
+    E = spec["embeddingSize"]
+    M = length * batch
+    hh = int(head["hidden"])
+    K16 = math.ceil(K / 16)
+    segments.append({"name": "head", "prefix": "head.", "ops": [
+        {"name": "gather", "kernel": "gather", "constants": {"K": markers, "D": H, "L": length},
+         "bind": ["packed", stream, "states"], "dispatch": [1, 1]},
+        mm("fc1", K, hh, H, 1, ["states", "w:head.fc1.weight", "w:head.fc1.bias", "h1"], K16),
+        mm("fc2", K, 1, hh, 0, ["h1", "w:head.fc2.weight", "w:head.fc2.bias", "raw"], K16),
+        {"name": "maskl", "kernel": "masklogits", "constants": {"K": markers, "TEMP": float(head["temperature"])},
+         "bind": ["raw", "packed", "logits"], "dispatch": [1, 1]},
+    ]})
+    all_ops = [op for s in segments for op in s.get("captureOps", []) + s["ops"]]
+    cols: dict[str, int] = {}
+    for op in all_ops:
+        dst = op["bind"][writable_bindings(op["kernel"], len(op["bind"]))[0]]
+        n = _elements_written(op)
+        if n > 0:
+            cols[dst] = max(cols.get(dst, 0), n)
+    k_rows = {"states", "kNormed", "h1", "raw"}
+    decls = []
+
+    def st(bid, nbytes, usage="rw", init=None):
+        d = {"id": bid, "bytes": int(nbytes), "usage": usage}
+        if init is not None:
+            d["init"] = init
+        decls.append(d)
+
+    emb = spec["embed"]
+    st("emb", bytes_of(M * E))
+    if absolute or emb["typeVocab"] > 0:
+        st("typeIds", M * 4)
+    for bid in ("x", "tmp"):
+        if bid in cols:
+            st(bid, bytes_of(M * cols[bid]), "rwSrc")
+    for bid in ("normed", "qkv", "ctx", "attnOut", "mid", "gate", "ffnOut", "states", "kNormed", "h1", "raw"):
+        if bid in cols:
+            st(bid, bytes_of((K if bid in k_rows else M) * cols[bid]))
+    st("mask", M * 4)
+    if any("kinfo" in o["bind"] for o in all_ops):
+        st("kinfo", 8 * batch)
+    for bid in ("c2p", "p2c"):
+        rel_ops = [o for o in all_ops if o["kernel"] == "attrel" and o["bind"][4] == bid]
+        if rel_ops:
+            st(bid, max(o["constants"]["ROWS"] * o["constants"]["H"] * o["constants"]["NM"] * 4
+                        for o in rel_ops))
+    score_ops = [o for o in all_ops if o["kernel"] == "attscore"]
+    if score_ops:
+        st("scores", max(o["constants"]["ROWS"] * o["constants"]["H"] * o["constants"]["L"] * 4
+                         for o in score_ops))
+    if any("dummy" in o["bind"] for o in all_ops):
+        st("dummy", 4, "storage")
+    st("packed", 3 * K * 4)
+    st("logits", K * 4, "logits")
+    rel = spec["attention"].get("rel") if spec["attention"]["kind"] == "deberta-relative" else None
+    if rel is not None:
+        table = rel_pos_table(length, rel["buckets"], rel["maxPositions"])
+        st("relidx", table.nbytes, "rw", table)
+    rope = spec["attention"].get("rope")
+    if rope and rope["thetaGlobal"] == rope["thetaLocal"]:
+        table = rope_table(length, rope["thetaGlobal"], spec["headDim"])
+        st("cossin", table.nbytes, "rw", table)
+    elif rope:
+        g = rope_table(length, rope["thetaGlobal"], spec["headDim"])
+        lt = rope_table(length, rope["thetaLocal"], spec["headDim"])
+        st("cossinG", g.nbytes, "rw", g)
+        st("cossinL", lt.nbytes, "rw", lt)
+    zero_uses = [o for o in all_ops if "zero" in o["bind"]]
+    if zero_uses:
+        w = max(o["constants"]["N"] for o in zero_uses)
+        st("zero", bytes_of(w), "rw", np.zeros(bytes_of(w), dtype=np.uint8))
+    validate_segments(segments, {d["id"] for d in decls})
+    return {
+        "f16": f16, "length": length, "batch": batch, "markers": markers, "embeddingSize": E,
+        "buffers": decls, "segments": segments,
+        "inputs": {"embeddings": "emb", "mask": "mask", "markers": "packed"},
+        "output": {"buffer": "logits", "bytes": K * 4, "dtype": "f32", "rows": K, "cols": 1},
+        "captureSlots": 0, "captureSlotBytes": length * H * 4,
+    }
+
+
+def pack_markers(indices, mask, groups=None, markers: int | None = None) -> np.ndarray:
+    """The packed marker payload of one sequence (RunInput.packedMarkers, src/plan/executor.ts:28):
+    [0, K) marker row indices, [K, 2K) the marker mask as f32 bits, [2K, 3K) group ids; the
+    payloads of a batch plan follow each other. Shorter lists are padded with masked slots."""
+    idx = np.asarray(indices, dtype=np.uint32)
+    K = len(idx) if markers is None else markers
+    if len(idx) > K:
+        raise ValueError(f"{len(idx)} markers, the plan holds {K}")
+    out = np.zeros(3 * K, dtype=np.uint32)
+    out[:len(idx)] = idx
+    out[K:K + len(idx)] = np.asarray(mask, dtype=np.float32).view(np.uint32)
+    if groups is not None:
+        out[2 * K:2 * K + len(idx)] = np.asarray(groups, dtype=np.uint32)
+    return out
+
+
 def plan_json(plan: dict) -> dict:
     """The plan without its typed-array init tables (they travel as separate byte buffers)."""
     out = dict(plan)
@@ -321,5 +435,5 @@ def all_ops(plan: dict) -> list[dict]:
     return [op for s in plan["segments"] for op in s["ops"]]
 
 
-__all__ = ["build_plan", "plan_json", "plan_inits", "rel_pos_table", "rope_table",
+__all__ = ["build_plan", "pack_markers", "plan_json", "plan_inits", "rel_pos_table", "rope_table",
            "rel_bucket_index", "act_code", "all_ops", "add_workgroups"]

@@ -213,6 +213,11 @@ def manifest_tensors(spec: dict, head: dict) -> list[tuple[str, tuple[int, ...],
         out.append((names.finalNormW, (H,), "gamma"))
         if names.finalNormB:
             out.append((names.finalNormB, (H,), "beta"))
+    if head["type"] == "gliner2":
+        # the span head's two products (src/plan/build.ts:367-370)
+        hh = int(head["hidden"])
+        out += [("head.fc1.weight", (hh, H), "matrix"), ("head.fc1.bias", (hh,), "bias"),
+                ("head.fc2.weight", (1, hh), "matrix"), ("head.fc2.bias", (1,), "bias")]
     for step in head.get("steps", []):
         if step["op"] == "dense":
             out.append((f"{step['name']}.weight", (step["out"], step["in"]), "matrix"))

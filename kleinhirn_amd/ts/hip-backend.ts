@@ -36,6 +36,7 @@ export interface KhAddon {
   planDestroy(plan: KhHandle): void;
   upload(plan: KhHandle, embeddings: ArrayBufferView, mask: Float32Array, typeIds: Uint32Array | null): void;
   uploadIds(plan: KhHandle, ids: Int32Array, mask: Float32Array, typeIds: Uint32Array | null): void;
+  uploadMarkers(plan: KhHandle, packed: Uint32Array): void;
   run(plan: KhHandle, rows: number): void;
   readOutput(plan: KhHandle): Float32Array;
   readOutputAsync(plan: KhHandle): Promise<Float32Array>;
@@ -122,7 +123,11 @@ export class HipPlanRunner implements PlanRunner {
   }
 
   upload(input: RunInput): void {
-    if (input.packedMarkers) throw new Error('marker inputs (GLiNER, Julia) are outside the HIP encoder heads');
+    // the reference's upload order and messages (src/plan/executor.ts:385-392)
+    if (this.plan.inputs.markers) {
+      if (!input.packedMarkers) throw new Error('plan needs packedMarkers');
+      this.kh.uploadMarkers(this.handle(), input.packedMarkers);
+    }
     if (this.plan.inputs.typeIds && !input.typeIds) throw new Error('plan needs typeIds');
     this.kh.upload(this.handle(), input.embeddings, input.mask, input.typeIds ?? null);
   }

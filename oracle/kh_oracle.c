@@ -45,6 +45,7 @@
 #define KHO_ATTSOFTREL 15
 #define KHO_ATTSTD 16
 #define KHO_ATTRELF 17
+#define KHO_MASKLOGITS 18
 
 /* One op record: pointer arguments, integer arguments, float arguments in the order the
  * reference's host encodes them (src/plan/wasm.ts:330-407). */
@@ -311,6 +312,17 @@ static void gather(const uint32_t *markers, const float *x, float *states, int K
     int b = g / K;
     long row = (long)b * L + markers[b * 3 * K + (g - b * K)];
     memcpy(states + (size_t)g * D, x + (size_t)row * D, (size_t)D * 4);
+  }
+}
+
+/* logits[k] = raw[k] / temp where the marker's mask word (f32 bits at b * 3K + K + k mod K, b = k / K)
+ * exceeds 0.5, else -1e4 (src/wasm/plan.ts:545-551) */
+static void masklogits(const float *raw, const uint32_t *packed, float *logits, int K, float temp, int total) {
+  for (int k = 0; k < total; k++) {
+    int b = k / K;
+    float m;
+    memcpy(&m, packed + (size_t)b * 3 * K + K + (k - b * K), 4);
+    logits[k] = m > 0.5f ? raw[k] / temp : -1e4f;
   }
 }
 
@@ -662,6 +674,9 @@ static void serial(const kho_ctx *cx, const kho_op *op, int n, float *scratch) {
   case KHO_GATHER:
     gather((const uint32_t *)p[0], (const float *)p[1], (float *)p[2], v[0], v[1], v[2], v[3]);
     break;
+  case KHO_MASKLOGITS:
+    masklogits((const float *)p[0], (const uint32_t *)p[1], (float *)p[2], v[0], op->f[0], v[1]);
+    break;
   case KHO_POOL:
     pool((const float *)p[0], (const float *)p[1], (float *)p[2], v[0], v[1], v[2], v[3]);
     break;
@@ -783,7 +798,7 @@ int kho_run(const kho_op *ops, int nops, int L, int batch, const float *mask, in
   kho_ctx cx = {L, batch, rows, mask, kinfo, scratch, scratch_per_thread,
                 rb > 0 ? rb : 16, cb > 0 ? cb : 64, qb > 0 ? qb : 32, min_work > 0 ? min_work : 65536};
   for (int o = 0; o < nops; o++)
-    if (ops[o].code < 1 || ops[o].code > KHO_ATTRELF || ops[o].code == 10) return -1;
+    if (ops[o].code < 1 || ops[o].code > KHO_MASKLOGITS || ops[o].code == 10) return -1;
   key_ranges(mask, kinfo, L, batch);
   for (int o = 0; o < nops; o++) {
     const kho_op *op = &ops[o];

@@ -24,7 +24,7 @@ LIB_PATH = os.path.join(HERE, "libkh_oracle.so")
 MATMUL = {"matmul", "mmtile", "mmtile8", "mmtile16"}
 CODE = {"gemmP": 1, "gemmNT": 2, "layernorm": 3, "embln": 4, "add": 5, "gather": 6, "pool": 7,
         "geglu": 8, "rope": 9, "attscore": 11, "attsoftmax": 12, "attpv": 13, "attrel": 14,
-        "attsoftrel": 15, "attstd": 16, "attrelf": 17}
+        "attsoftrel": 15, "attstd": 16, "attrelf": 17, "masklogits": 18}
 PAD_FLOATS = 16  # 64 spare bytes per allocation
 
 
@@ -220,6 +220,11 @@ class OraclePlan:
             code, rows = CODE["gather"], -1
             nbytes = next(x["bytes"] for x in self.plan["buffers"] if x["id"] == op["bind"][0])
             ptr, ints = [b(0), b(1), b(2)], [c["K"], c["D"], c["L"], nbytes // 12]
+        elif k == "masklogits":
+            # total = the marker buffer's u32 count / 3 (src/plan/wasm.ts:393-394)
+            code, rows = CODE["masklogits"], -1
+            nbytes = next(x["bytes"] for x in self.plan["buffers"] if x["id"] == op["bind"][1])
+            ptr, ints, fl = [b(0), b(1), b(2)], [c["K"], nbytes // 12], [c["TEMP"]]
         elif k == "pool":
             code, rows = CODE["pool"], -1
             ptr, ints = [b(0), b(1), b(2)], [c["L"], c["N"], c["MODE"], op["dispatch"][1]]
@@ -268,7 +273,8 @@ class OraclePlan:
         for i, v in enumerate(fl):
             r.f[i] = float(v)
 
-    def upload(self, embeddings: np.ndarray, mask: np.ndarray, type_ids: np.ndarray | None = None) -> None:
+    def upload(self, embeddings: np.ndarray, mask: np.ndarray, type_ids: np.ndarray | None = None,
+               markers: np.ndarray | None = None) -> None:
         """Copies the inputs into the plan's buffers (src/plan/wasm.ts:409-440)."""
         inp = self.plan["inputs"]
 
@@ -288,6 +294,10 @@ class OraclePlan:
             if type_ids is None:
                 raise ValueError("plan needs typeIds")
             put(inp["typeIds"], np.asarray(type_ids, dtype=np.uint32))
+        if "markers" in inp:
+            if markers is None:
+                raise ValueError("plan needs packed markers")
+            put(inp["markers"], np.asarray(markers, dtype=np.uint32))
 
     def run(self, rows: int, rb: int = 16, cb: int = 64, qb: int = 32, min_work: int = 1 << 16) -> None:
         if rows < 1 or rows > self.length * self.batch:

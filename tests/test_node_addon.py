@@ -55,6 +55,26 @@ def test_node_path_matches_python_path_and_golden():
     assert d["mismatched"] == 0, d
 
 
+@pytest.mark.gpu
+def test_node_gliner_head_matches_python_path():
+    """A GLiNER2 span head through the addon (uploadMarkers, the f32 logits) equals the Python
+    host's run of the same plan and payloads."""
+    from tests import gliner_case as G
+    from tests.test_gpu_gliner import hip_logits
+    c, W = G.case(3)
+    packed = G.payloads(c.ids)
+    S = configs.storage(W, True)
+    plan = build_plan(c.spec, G.HEAD, G.LENGTH, len(c.ids), True)
+    ri = inputs.run_input(c.spec, S["embeddings.word.weight"], c.ids, G.LENGTH)
+    ri["packedMarkers"] = np.concatenate(packed)
+    with tempfile.TemporaryDirectory() as d:
+        export_case(d, plan, S, ri, rows=G.LENGTH * len(c.ids))
+        res = run_node(d)
+        got = np.fromfile(os.path.join(d, "out.bin"), dtype=np.float32).reshape(len(c.ids), -1)
+    assert res["ok"]
+    assert np.array_equal(got, hip_logits(c, W, packed, True))
+
+
 def test_node_addon_checks_a_manifest_directory():
     """manifestCheck through the addon reads what kh_manifest_check reads."""
     from kleinhirn_amd import backend as B

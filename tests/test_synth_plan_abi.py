@@ -185,10 +185,10 @@ def test_every_benchmark_plan_lowers(name):
 def test_plan_check_names_unsupported_ops_and_bad_json():
     from kleinhirn_amd.backend import lib
     plan = build_plan(configs.roberta_base_spec(), S.roberta_classify_head(768, 3), 64, 1, True)
-    plan["segments"][1]["ops"].append({"name": "maskl", "kernel": "masklogits", "constants": {"K": 1, "TEMP": 1.0},
+    plan["segments"][1]["ops"].append({"name": "conv", "kernel": "im2col", "constants": {"N": 768, "KS": 3, "L": 64},
                                        "bind": ["qkv", "mask", "x"], "dispatch": [1, 1]})
     rc, msg = _check(plan)
-    assert rc == 2 and "maskl" in msg and "masklogits" in msg
+    assert rc == 2 and "conv" in msg and "im2col" in msg
     bad = b'{"segments": [}'
     assert lib().kh_plan_check(None, bad, len(bad)) == 1
     assert "plan JSON" in lib().kh_last_error().decode()
