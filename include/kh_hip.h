@@ -204,6 +204,13 @@ int kh_upload_ids(kh_plan *plan, const int32_t *ids, size_t id_count, const floa
  * sequence's valid rows gathers a zero state (the reference reads the padding row's state). */
 int kh_upload_markers(kh_plan *plan, const uint32_t *packed, size_t count);
 
+/* The qtype part of PlanRunner.upload (RunInput.qtype, src/plan/executor.ts:30-31) for plans with
+ * a rowSelect (the Julia head): type row qtype[b] of the rowSelect table is copied to row b of
+ * its destination before the forward (src/plan/executor.ts:236-246, src/plan/wasm.ts:429-439);
+ * count <= batch, sequences without an entry take row 0; a qtype past the table is KH_EINVAL at
+ * kh_run. */
+int kh_upload_qtypes(kh_plan *plan, const uint32_t *qtype, size_t count);
+
 /* PlanRunner.run (src/plan/executor.ts:295-297): one forward over `rows` rows (the real rows of
  * a B = 1 call, L * B for a batch plan), enqueued on the plan's stream; returns without waiting.
  * A batch call with fewer than KH_SPLIT_T (environment, default 65536) valid rows runs as two

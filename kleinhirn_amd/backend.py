@@ -27,7 +27,7 @@ ERRORS = {1: "EINVAL", 2: "EUNSUPPORTED", 3: "EHIP", 4: "ENOMEM", 5: "ELOST"}
 EXPORTS = [
     "kh_last_error", "kh_abi_version", "kh_ctx_create", "kh_ctx_destroy", "kh_weight_add",
     "kh_ctx_weight_bytes", "kh_words_set", "kh_plan_check", "kh_plan_create", "kh_plan_init_buffer",
-    "kh_plan_info_get", "kh_upload", "kh_upload_ids", "kh_upload_markers", "kh_run", "kh_read_output", "kh_sync",
+    "kh_plan_info_get", "kh_upload", "kh_upload_ids", "kh_upload_markers", "kh_upload_qtypes", "kh_run", "kh_read_output", "kh_sync",
     "kh_last_run_ms", "kh_profile", "kh_packed_rows", "kh_plan_destroy", "kh_manifest_check",
     "kh_load_manifest", "kh_sha256", "kh_row_checksum", "kh_scores", "kh_read_scores", "kh_rank",
     "kh_sched_create", "kh_sched_run", "kh_sched_destroy", "kh_trace", "kh_trace_read",
@@ -103,6 +103,7 @@ def lib() -> ctypes.CDLL:
         "kh_upload": [vp, vp, sz, vp, sz, vp, sz],
         "kh_upload_ids": [vp, vp, sz, vp, sz, vp, sz],
         "kh_upload_markers": [vp, vp, sz],
+        "kh_upload_qtypes": [vp, vp, sz],
         "kh_run": [vp, i32],
         "kh_read_output": [vp, vp, sz],
         "kh_sync": [vp],
@@ -224,9 +225,20 @@ class HipPlanRunner:
         packed = np.ascontiguousarray(packed, dtype=np.uint32)
         _check(lib().kh_upload_markers(self.h, _ptr(packed), packed.size))
 
+    def _qtypes(self, qtype) -> None:
+        # RunInput.qtype of plans with a rowSelect: one number, or one per sequence
+        if not self.plan.get("rowSelect"):
+            return
+        q = np.atleast_1d(np.asarray(0 if qtype is None else qtype, dtype=np.int64))
+        if np.any(q < 0):
+            raise ValueError("qtype must not be negative")
+        q = np.ascontiguousarray(q, dtype=np.uint32)
+        _check(lib().kh_upload_qtypes(self.h, _ptr(q), q.size))
+
     def upload(self, inp: dict) -> None:
-        """RunInput {embeddings, mask, typeIds?, packedMarkers?} (src/plan/executor.ts:25-32)."""
+        """RunInput {embeddings, mask, typeIds?, packedMarkers?, qtype?} (src/plan/executor.ts:25-32)."""
         self._markers(inp.get("packedMarkers"))
+        self._qtypes(inp.get("qtype"))
         emb = np.ascontiguousarray(inp["embeddings"])
         want = np.float16 if self.plan["f16"] else np.float32
         if emb.dtype != want:
@@ -238,8 +250,9 @@ class HipPlanRunner:
                                0 if tt is None else tt.size))
 
     def upload_ids(self, ids: np.ndarray, mask: np.ndarray, type_ids: np.ndarray | None = None,
-                   packed_markers: np.ndarray | None = None) -> None:
+                   packed_markers: np.ndarray | None = None, qtype=None) -> None:
         self._markers(packed_markers)
+        self._qtypes(qtype)
         ids = np.ascontiguousarray(ids, dtype=np.int32)
         mask = np.ascontiguousarray(mask, dtype=np.float32)
         tt = None if type_ids is None else np.ascontiguousarray(type_ids, dtype=np.uint32)

@@ -186,6 +186,10 @@ struct kh_plan {
   std::vector<uint32_t> markers_host;  // the last kh_upload_markers payload
   bool markers_dirty = false;
   bool out_f32 = false;                // output buffer holds f32 whatever the storage dtype
+  // rowSelect (Julia): row qtype[b] of the table weight copied to row b of dst before each run
+  std::string rs_table, rs_dst;
+  int64_t rs_row_bytes = 0;
+  std::vector<uint32_t> qtype_host;
   std::string out_buf;
   int out_rows = 0, out_cols = 0;
   bool out_packed = false;
@@ -1056,6 +1060,20 @@ static void pack(kh_plan *pl, int rows, int b_end) {
     if (pl->d_tt.bytes < tt.size() * 4 || !pl->d_tt.p) pl->d_tt.alloc(tt.size() * 4);
     put(pl->d_tt, tt.data(), tt.size() * 4);
   }
+  // rowSelect: the type row of each sequence (device-to-device, ordered before the forward)
+  if (!pl->rs_dst.empty()) {
+    const Weight *w = weight_of(pl->ctx, pl->rs_table);
+    const int64_t rows = w->count * (pl->f16 ? 2 : 4) / pl->rs_row_bytes;
+    char *dst = (char *)pl->bufs.at(pl->rs_dst).mem->p;
+    for (int b = 0; b < B; b++) {
+      const uint32_t q = pl->qtype_host[b];
+      if ((int64_t)q >= rows)
+        fail(KH_EINVAL, "qtype " + std::to_string(q) + " of sequence " + std::to_string(b) + " outside the " +
+                            std::to_string(rows) + " rows of " + pl->rs_table.substr(2));
+      KH_CHECK(hipMemcpyAsync(dst + (size_t)b * pl->rs_row_bytes, (const char *)w->mem->p + (size_t)q * pl->rs_row_bytes,
+                              pl->rs_row_bytes, hipMemcpyDeviceToDevice, pl->stream));
+    }
+  }
   // packed marker payloads: B blocks of 3 K u32 (row indices, mask bits, groups), rows within L
   if (!pl->in_markers.empty()) {
     const int K = pl->markers;
@@ -1616,8 +1634,6 @@ int kh_plan_check(kh_ctx *ctx, const char *plan_json, size_t len) {
   std::vector<std::string> errors;
   auto steps = lower(pp, f16, L, errors);
   if (ctx) check_bindings(ctx, pp, steps, f16, errors);
-  if (pp.root.has("rowSelect") && pp.root.at("rowSelect").kind != Json::Null)
-    errors.push_back("rowSelect (Julia type rows) is outside the encoder heads");
   if (!errors.empty()) fail(KH_EUNSUPPORTED, join_errors(errors));
   KH_API_END
 }
@@ -1645,6 +1661,19 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
     pl->in_markers = inputs.at("markers").str();
     if (pl->markers < 1) fail(KH_EINVAL, "a plan with a markers input needs markers >= 1");
   }
+  if (pp.root.has("rowSelect") && pp.root.at("rowSelect").kind != Json::Null) {
+    const Json &rs = pp.root.at("rowSelect");
+    pl->rs_table = rs.at("table").str();
+    pl->rs_dst = rs.at("dst").str();
+    pl->rs_row_bytes = rs.at("rowBytes").integer();
+    const Weight *w = weight_of(ctx, pl->rs_table);
+    const int64_t es = pl->f16 ? 2 : 4;
+    if (!w) fail(KH_EINVAL, "rowSelect table " + pl->rs_table + " missing");
+    if (w->dtype != (pl->f16 ? KH_F16 : KH_F32) || pl->rs_row_bytes <= 0 || pl->rs_row_bytes % es ||
+        w->count * es < pl->rs_row_bytes)
+      fail(KH_EINVAL, "rowSelect table " + pl->rs_table + " does not hold rows of " + std::to_string(pl->rs_row_bytes) + " B");
+    pl->qtype_host.assign(pl->B, 0u);
+  }
   pl->in_emb = inputs.at("embeddings").str();
   pl->out_buf = pp.root.at("output").at("buffer").str();
   if (!getenv("KH_NO_FUSION")) fuse_steps(pl.get());
@@ -1670,6 +1699,9 @@ int kh_plan_create(kh_ctx *ctx, const char *plan_json, size_t len, kh_plan **out
     if (!pl->bufs.count(pl->in_markers) || pl->bufs.at(pl->in_markers).bytes < (int64_t)pl->markers_host.size() * 4)
       fail(KH_EINVAL, "markers buffer smaller than 3 * markers * batch u32");
   }
+  if (!pl->rs_dst.empty() &&
+      (!pl->bufs.count(pl->rs_dst) || pl->bufs.at(pl->rs_dst).bytes < pl->rs_row_bytes * pl->B))
+    fail(KH_EINVAL, "rowSelect destination smaller than batch rows");
   if (!getenv("KH_NO_PRUNE")) prune_tail(pl.get());
   // row spaces and uses
   pl->bufs.at(pl->in_emb).packed_space = true;
@@ -1878,6 +1910,20 @@ int kh_upload_markers(kh_plan *plan, const uint32_t *packed, size_t count) {
                         std::to_string(plan->markers) + " * " + std::to_string(plan->B) + " = " + std::to_string(want));
   memcpy(plan->markers_host.data(), packed, want * 4);
   plan->dirty = true;  // the payload travels with the next run's packed metadata
+  KH_API_END
+}
+
+int kh_upload_qtypes(kh_plan *plan, const uint32_t *qtype, size_t count) {
+  KH_API_BEGIN
+  if (!plan) fail(KH_EINVAL, "null plan");
+  require_live(plan->ctx);
+  if (plan->rs_dst.empty()) fail(KH_EINVAL, "the plan has no rowSelect (type rows)");
+  if (count > (size_t)plan->B || (count && !qtype))
+    fail(KH_EINVAL, std::to_string(count) + " qtypes, the plan has " + std::to_string(plan->B) + " sequences");
+  // sequences without an entry take row 0 (qtypes[b] ?? 0)
+  std::fill(plan->qtype_host.begin(), plan->qtype_host.end(), 0u);
+  if (count) memcpy(plan->qtype_host.data(), qtype, count * 4);
+  plan->dirty = true;
   KH_API_END
 }
 

@@ -347,6 +347,23 @@ static napi_value upload_markers(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* uploadQtypes(plan, qtype: Uint32Array): RunInput.qtype of a rowSelect (Julia) plan */
+static napi_value upload_qtypes(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return NULL;
+  handle *h = unwrap(env, argv[0], 2);
+  if (!h) return NULL;
+  void *q;
+  size_t qb;
+  if (!get_bytes(env, argv[1], &q, &qb)) {
+    napi_throw_type_error(env, NULL, "uploadQtypes takes a Uint32Array");
+    return NULL;
+  }
+  int rc = kh_upload_qtypes((kh_plan *)h->ptr, (const uint32_t *)q, qb / 4);
+  if (rc) return throw_kh(env, rc);
+  return NULL;
+}
+
 static napi_value run(napi_env env, napi_callback_info info) {
   napi_value argv[2];
   if (!get_args(env, info, 2, argv)) return NULL;
@@ -657,6 +674,7 @@ static napi_value init(napi_env env, napi_value exports) {
       {"upload", 0, upload, 0, 0, 0, napi_default, 0},
       {"uploadIds", 0, upload_ids, 0, 0, 0, napi_default, 0},
       {"uploadMarkers", 0, upload_markers, 0, 0, 0, napi_default, 0},
+      {"uploadQtypes", 0, upload_qtypes, 0, 0, 0, napi_default, 0},
       {"run", 0, run, 0, 0, 0, napi_default, 0},
       {"readOutput", 0, read_output, 0, 0, 0, napi_default, 0},
       {"readOutputAsync", 0, read_output_async, 0, 0, 0, napi_default, 0},

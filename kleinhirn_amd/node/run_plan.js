@@ -47,6 +47,7 @@ if (meta.checkOnly) {
   const tt = meta.typeIds ? typed(read('tt.bin'), Uint32Array) : null;
   const mask = typed(read('mask.bin'), Float32Array);
   if (meta.markers) addon.uploadMarkers(plan, typed(read('mk.bin'), Uint32Array));
+  if (meta.qtype) addon.uploadQtypes(plan, Uint32Array.from(meta.qtype));
   if (meta.ids) addon.uploadIds(plan, typed(read('ids.bin'), Int32Array), mask, tt);
   else addon.upload(plan, read('emb.bin'), mask, tt);
   addon.run(plan, meta.rows);

@@ -48,6 +48,8 @@ def export_case(dirname: str, plan: dict, weights: dict | None = None, run_input
             np.ascontiguousarray(run_input["typeIds"], dtype=np.uint32).tofile(os.path.join(dirname, "tt.bin"))
         if meta["markers"]:
             np.ascontiguousarray(run_input["packedMarkers"], dtype=np.uint32).tofile(os.path.join(dirname, "mk.bin"))
+        if run_input.get("qtype") is not None:
+            meta["qtype"] = [int(x) for x in np.atleast_1d(run_input["qtype"])]
     with open(os.path.join(dirname, "meta.json"), "w") as f:
         json.dump(meta, f)
 

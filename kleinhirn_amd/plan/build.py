@@ -13,7 +13,7 @@ import math
 import numpy as np
 
 from .layers import add_workgroups, post_norm_layer, pre_norm_layer
-from .spec import tensor_names_for
+from .spec import julia_head_layer, tensor_names_for
 
 ACT = {"relu": 1, "gelu": 2, "tanh": 3, "silu": 4}
 
@@ -100,12 +100,15 @@ def build_plan(spec: dict, head: dict, length: int, batch: int, f16: bool, marke
     """src/plan/build.ts:109-526 for classify, token, embed and GLiNER2 heads. `markers` is the
     reference's BuildOptions.markers (marker slots per sequence of a GLiNER2 plan; the head's own
     count when None)."""
-    if head["type"] not in ("classify", "token", "embed", "gliner2"):
+    if head["type"] not in ("classify", "token", "embed", "gliner2", "julia"):
         raise ValueError(f"head {head['type']} is not an encoder head of this runner")
-    pooled = head["type"] != "gliner2"
-    markers = 0 if pooled else int(head["markers"] if markers is None else markers)
+    pooled = head["type"] not in ("gliner2", "julia")
+    if head["type"] == "julia":
+        markers = int(head["options"])
+    else:
+        markers = 0 if pooled else int(head["markers"] if markers is None else markers)
     if not pooled and markers < 1:
-        raise ValueError("a GLiNER2 plan needs at least one marker slot")
+        raise ValueError("a marker head needs at least one marker slot")
     K = markers * batch
     names = tensor_names_for(spec)
     H = spec["hidden"]
@@ -190,7 +193,8 @@ def build_plan(spec: dict, head: dict, length: int, batch: int, f16: bool, marke
         stream = "tmp"
 
     if not pooled:
-        return _gliner2_plan(spec, head, segments, stream, length, batch, f16, markers, K, bytes_of, mm, absolute)
+        return _marker_plan(spec, head, segments, stream, dims, length, batch, f16, markers, K, bytes_of, mm, ln,
+                            absolute)
 
     # Head (src/plan/build.ts:296-357)
     head_buffers = []
@@ -316,25 +320,52 @@ def build_plan(spec: dict, head: dict, length: int, batch: int, f16: bool, marke
     }
 
 
-def _gliner2_plan(spec, head, segments, stream, length, batch, f16, markers, K, bytes_of, mm, absolute) -> dict:
-    """The GLiNER2 span head (src/plan/build.ts:358-377): the hidden states at the K = markers x
-    batch marker rows (gather over the packed markers input: per sequence K indices, K mask words
-    as f32 bits, K group ids), fc1 with ReLU, fc2 to one raw logit per marker, and masklogits
-    (raw / temperature where the marker's mask is set, else -1e4) into an f32 output. Buffers as
-    src/plan/build.ts:432-526 lays them out for a marker head."""
+def _marker_plan(spec, head, segments, stream, dims, length, batch, f16, markers, K, bytes_of, mm, ln,
+                 absolute) -> dict:
+    """Marker heads, whose output is one f32 logit per marker slot (K = markers x batch slots; the
+    packed markers input holds per sequence K row indices, K mask words as f32 bits, K group ids):
+    * gliner2 (src/plan/build.ts:358-377): the hidden states at the marker rows, fc1 with ReLU,
+      fc2 to one raw logit, masklogits (raw / temperature where the mask is set, else -1e4);
+    * julia (src/plan/build.ts:378-430): the type row of each sequence (rowSelect of type_emb by
+      the run's qtype) added to every row of the final-norm stream, `layers` pre-norm layers with
+      an MLP of width `ffn` (ReLU) and full attention without RoPE, then the scorer: gather,
+      LayerNorm, fc1 with GELU, fc2, masklogits at temperature 1.
+    Buffers as src/plan/build.ts:432-526 lays them out for a marker head."""
     H = spec["hidden"]
     E = spec["embeddingSize"]
     M = length * batch
-    hh = int(head["hidden"])
     K16 = math.ceil(K / 16)
-    segments.append({"name": "head", "prefix": "head.", "ops": [
-        {"name": "gather", "kernel": "gather", "constants": {"K": markers, "D": H, "L": length},
-         "bind": ["packed", stream, "states"], "dispatch": [1, 1]},
-        mm("fc1", K, hh, H, 1, ["states", "w:head.fc1.weight", "w:head.fc1.bias", "h1"], K16),
-        mm("fc2", K, 1, hh, 0, ["h1", "w:head.fc2.weight", "w:head.fc2.bias", "raw"], K16),
-        {"name": "maskl", "kernel": "masklogits", "constants": {"K": markers, "TEMP": float(head["temperature"])},
-         "bind": ["raw", "packed", "logits"], "dispatch": [1, 1]},
-    ]})
+    row_select = None
+    if head["type"] == "gliner2":
+        hh = int(head["hidden"])
+        segments.append({"name": "head", "prefix": "head.", "ops": [
+            {"name": "gather", "kernel": "gather", "constants": {"K": markers, "D": H, "L": length},
+             "bind": ["packed", stream, "states"], "dispatch": [1, 1]},
+            mm("fc1", K, hh, H, 1, ["states", "w:head.fc1.weight", "w:head.fc1.bias", "h1"], K16),
+            mm("fc2", K, 1, hh, 0, ["h1", "w:head.fc2.weight", "w:head.fc2.bias", "raw"], K16),
+            {"name": "maskl", "kernel": "masklogits", "constants": {"K": markers, "TEMP": float(head["temperature"])},
+             "bind": ["raw", "packed", "logits"], "dispatch": [1, 1]},
+        ]})
+    else:
+        if stream != "tmp":
+            raise ValueError("julia head expects a final norm")
+        segments.append({"name": "typed", "prefix": "", "ops": [
+            {"name": "type", "kernel": "add", "constants": {"TOTAL": M * H, "N": H, "MODE": 1, "L": length},
+             "bind": ["tmp", "typeRow"], "dispatch": [add_workgroups(M, H), 1]}]})
+        row_select = {"table": "w:type_emb.weight", "dst": "typeRow", "rowBytes": bytes_of(H)}
+        for i in range(int(head["layers"])):
+            segments.append({"name": f"head{i}", "prefix": f"head{i}.", "ops": pre_norm_layer(
+                dims, julia_head_layer(i), "tmp", True, (H / spec["heads"]) ** -0.5, 0, False,
+                {"kind": "mlp", "width": int(head["ffn"]), "act": 1})})
+        segments.append({"name": "scorer", "prefix": "scorer.", "ops": [
+            {"name": "gather", "kernel": "gather", "constants": {"K": markers, "D": H, "L": length},
+             "bind": ["packed", "tmp", "states"], "dispatch": [1, 1]},
+            ln("ln", 0, ["states", "dummy", "w:scorer.norm.weight", "w:scorer.norm.bias", "mask", "kNormed"], H, K),
+            mm("fc1", K, H, H, 2, ["kNormed", "w:scorer.fc1.weight", "w:scorer.fc1.bias", "h1"], K16),
+            mm("fc2", K, 1, H, 0, ["h1", "w:scorer.fc2.weight", "w:scorer.fc2.bias", "raw"], K16),
+            {"name": "maskl", "kernel": "masklogits", "constants": {"K": markers, "TEMP": 1.0},
+             "bind": ["raw", "packed", "logits"], "dispatch": [1, 1]},
+        ]})
     all_ops = [op for s in segments for op in s.get("captureOps", []) + s["ops"]]
     cols: dict[str, int] = {}
     for op in all_ops:
@@ -390,18 +421,23 @@ def _gliner2_plan(spec, head, segments, stream, length, batch, f16, markers, K, 
         lt = rope_table(length, rope["thetaLocal"], spec["headDim"])
         st("cossinG", g.nbytes, "rw", g)
         st("cossinL", lt.nbytes, "rw", lt)
+    if row_select:
+        st("typeRow", bytes_of(batch * H))
     zero_uses = [o for o in all_ops if "zero" in o["bind"]]
     if zero_uses:
         w = max(o["constants"]["N"] for o in zero_uses)
         st("zero", bytes_of(w), "rw", np.zeros(bytes_of(w), dtype=np.uint8))
     validate_segments(segments, {d["id"] for d in decls})
-    return {
+    plan = {
         "f16": f16, "length": length, "batch": batch, "markers": markers, "embeddingSize": E,
         "buffers": decls, "segments": segments,
         "inputs": {"embeddings": "emb", "mask": "mask", "markers": "packed"},
         "output": {"buffer": "logits", "bytes": K * 4, "dtype": "f32", "rows": K, "cols": 1},
         "captureSlots": 0, "captureSlotBytes": length * H * 4,
     }
+    if row_select:
+        plan["rowSelect"] = row_select
+    return plan
 
 
 def pack_markers(indices, mask, groups=None, markers: int | None = None) -> np.ndarray:

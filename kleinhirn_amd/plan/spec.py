@@ -168,6 +168,43 @@ def modernbert(hidden: int, layers: int, heads: int, intermediate: int, vocab: i
     }
 
 
+def julia(hidden: int, layers: int, heads: int, intermediate: int, vocab: int, norm_eps: float,
+          rope_theta: float, local_attention: int, global_every: int, head_layers: int, head_ffn: int,
+          options: int, max_pos: int = 0) -> tuple[dict, dict]:
+    """specFromJuliaManifest (src/plan/spec.ts:248-277): a ModernBERT encoder with one RoPE theta,
+    window half = localAttention, no biases, a final norm; the julia head (type row, head layers,
+    scorer over `options` marker slots)."""
+    head_dim = hidden // heads
+    norm = {"eps": norm_eps, "bias": False}
+    spec = {
+        "family": "modernbert", "hidden": hidden, "layers": layers, "heads": heads,
+        "headDim": head_dim, "intermediate": intermediate, "vocab": vocab, "embeddingSize": hidden,
+        "embed": {"positions": "none", "positionOffset": 0, "maxPositions": max_pos,
+                  "typeVocab": 0, "norm": norm, "maskMultiply": False, "project": False},
+        "attention": {"kind": "standard", "bias": False, "scale": head_dim ** -0.5,
+                      "rope": {"thetaGlobal": rope_theta, "thetaLocal": rope_theta},
+                      "window": {"half": local_attention, "globalEvery": global_every}},
+        "block": {"order": "pre", "firstNormIdentity": True, "finalNorm": True, "norm": norm},
+        "ffn": {"kind": "geglu", "act": "gelu", "bias": False},
+    }
+    return spec, {"type": "julia", "layers": head_layers, "ffn": head_ffn, "options": options}
+
+
+# rows of the Julia type table: the request types choice, score, noul (src/tokenizer/julia-input.ts:21)
+JULIA_TYPES = 3
+
+
+def julia_head_layer(i: int) -> dict:
+    """Tensor names of Julia head layer i (src/plan/build.ts:387-396)."""
+    p = f"head.{i}"
+    return {"qkvW": f"{p}.in_proj.weight", "qkvB": f"{p}.in_proj.bias",
+            "attnOutW": f"{p}.out_proj.weight", "attnOutB": f"{p}.out_proj.bias",
+            "attnNormW": f"{p}.norm1.weight", "attnNormB": f"{p}.norm1.bias",
+            "ffnNormW": f"{p}.norm2.weight", "ffnNormB": f"{p}.norm2.bias",
+            "ffnInW": f"{p}.linear1.weight", "ffnInB": f"{p}.linear1.bias",
+            "ffnOutW": f"{p}.linear2.weight", "ffnOutB": f"{p}.linear2.bias"}
+
+
 def embed_head(pool: str, normalize: bool = True, steps=None) -> dict:
     """Embeddings head: pooling as sentence-transformers, optional dense steps
     (src/plan/hf.ts:272-278)."""
@@ -213,6 +250,23 @@ def manifest_tensors(spec: dict, head: dict) -> list[tuple[str, tuple[int, ...],
         out.append((names.finalNormW, (H,), "gamma"))
         if names.finalNormB:
             out.append((names.finalNormB, (H,), "beta"))
+    if head["type"] == "julia":
+        F = int(head["ffn"])
+        out.append(("type_emb.weight", (JULIA_TYPES, H), "table"))
+        for i in range(int(head["layers"])):
+            t = julia_head_layer(i)
+            for key, shape, kind in (
+                ("qkvW", (3 * H, H), "matrix"), ("qkvB", (3 * H,), "bias"),
+                ("attnOutW", (H, H), "matrix"), ("attnOutB", (H,), "bias"),
+                ("attnNormW", (H,), "gamma"), ("attnNormB", (H,), "beta"),
+                ("ffnNormW", (H,), "gamma"), ("ffnNormB", (H,), "beta"),
+                ("ffnInW", (F, H), "matrix"), ("ffnInB", (F,), "bias"),
+                ("ffnOutW", (H, F), "matrix"), ("ffnOutB", (H,), "bias"),
+            ):
+                out.append((t[key], shape, kind))
+        out += [("scorer.norm.weight", (H,), "gamma"), ("scorer.norm.bias", (H,), "beta"),
+                ("scorer.fc1.weight", (H, H), "matrix"), ("scorer.fc1.bias", (H,), "bias"),
+                ("scorer.fc2.weight", (1, H), "matrix"), ("scorer.fc2.bias", (1,), "bias")]
     if head["type"] == "gliner2":
         # the span head's two products (src/plan/build.ts:367-370)
         hh = int(head["hidden"])

@@ -37,6 +37,7 @@ export interface KhAddon {
   upload(plan: KhHandle, embeddings: ArrayBufferView, mask: Float32Array, typeIds: Uint32Array | null): void;
   uploadIds(plan: KhHandle, ids: Int32Array, mask: Float32Array, typeIds: Uint32Array | null): void;
   uploadMarkers(plan: KhHandle, packed: Uint32Array): void;
+  uploadQtypes(plan: KhHandle, qtype: Uint32Array): void;
   run(plan: KhHandle, rows: number): void;
   readOutput(plan: KhHandle): Float32Array;
   readOutputAsync(plan: KhHandle): Promise<Float32Array>;
@@ -127,6 +128,11 @@ export class HipPlanRunner implements PlanRunner {
     if (this.plan.inputs.markers) {
       if (!input.packedMarkers) throw new Error('plan needs packedMarkers');
       this.kh.uploadMarkers(this.handle(), input.packedMarkers);
+    }
+    if (this.plan.rowSelect) {
+      // Julia: one type row per sequence (qtypes[b] ?? 0)
+      const q = Array.isArray(input.qtype) ? input.qtype : [input.qtype ?? 0];
+      this.kh.uploadQtypes(this.handle(), Uint32Array.from(q));
     }
     if (this.plan.inputs.typeIds && !input.typeIds) throw new Error('plan needs typeIds');
     this.kh.upload(this.handle(), input.embeddings, input.mask, input.typeIds ?? null);

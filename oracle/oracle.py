@@ -274,7 +274,7 @@ class OraclePlan:
             r.f[i] = float(v)
 
     def upload(self, embeddings: np.ndarray, mask: np.ndarray, type_ids: np.ndarray | None = None,
-               markers: np.ndarray | None = None) -> None:
+               markers: np.ndarray | None = None, qtype=None) -> None:
         """Copies the inputs into the plan's buffers (src/plan/wasm.ts:409-440)."""
         inp = self.plan["inputs"]
 
@@ -298,6 +298,16 @@ class OraclePlan:
             if markers is None:
                 raise ValueError("plan needs packed markers")
             put(inp["markers"], np.asarray(markers, dtype=np.uint32))
+        rs = self.plan.get("rowSelect")
+        if rs:
+            # the type row of each sequence (src/plan/wasm.ts:429-439): qtypes[b] ?? 0
+            q = list(qtype) if isinstance(qtype, (list, tuple, np.ndarray)) else [qtype or 0]
+            table = self.rt.w[rs["table"][2:]].reshape(-1)
+            n = rs["rowBytes"] // 4
+            dst = self.bufs[rs["dst"]]
+            for b in range(self.batch):
+                r = int(q[b]) if b < len(q) else 0
+                dst[b * n:(b + 1) * n] = table[r * n:(r + 1) * n]
 
     def run(self, rows: int, rb: int = 16, cb: int = 64, qb: int = 32, min_work: int = 1 << 16) -> None:
         if rows < 1 or rows > self.length * self.batch:

@@ -75,6 +75,26 @@ def test_node_gliner_head_matches_python_path():
     assert np.array_equal(got, hip_logits(c, W, packed, True))
 
 
+@pytest.mark.gpu
+def test_node_julia_head_matches_python_path():
+    """The Julia head through the addon (uploadMarkers, uploadQtypes) equals the Python host."""
+    from tests import julia_case as J
+    from tests.test_gpu_julia import hip_logits
+    ids, W = J.case(3)
+    packed, qtypes = J.payloads(ids)
+    S = configs.storage(W, True)
+    plan = build_plan(J.SPEC, J.HEAD, J.LENGTH, len(ids), True)
+    ri = inputs.run_input(J.SPEC, S["embeddings.word.weight"], ids, J.LENGTH)
+    ri["packedMarkers"] = np.concatenate(packed)
+    ri["qtype"] = qtypes
+    with tempfile.TemporaryDirectory() as d:
+        export_case(d, plan, S, ri, rows=J.LENGTH * len(ids))
+        res = run_node(d)
+        got = np.fromfile(os.path.join(d, "out.bin"), dtype=np.float32).reshape(len(ids), -1)
+    assert res["ok"]
+    assert np.array_equal(got, hip_logits(ids, W, packed, qtypes, True))
+
+
 def test_node_addon_checks_a_manifest_directory():
     """manifestCheck through the addon reads what kh_manifest_check reads."""
     from kleinhirn_amd import backend as B
