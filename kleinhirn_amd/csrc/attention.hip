@@ -317,21 +317,34 @@ attn_kernel(AttnArgs a, Packing p) {
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  if (!qvalid) return;
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  T *out = (T *)a.ctx + (base + qi) * (int64_t)H * D + h * D;
+  // The output tile leaves through LDS (the K tile's space, free after the key loop's last
+  // barrier): a lane holds 4-value pieces of one query row, scattered over 32 rows per store;
+  // staged, every row goes out as whole 16-byte chunks.
+  constexpr int LDO = LDK;
+  static_assert(QT * LDO <= KT * LDK, "the output tile must fit the K tile");
+  T *sO = sK;
   typedef T vec4_t __attribute__((ext_vector_type(4)));
+  const int ql = w * 32 + (lane & 31);
 #pragma unroll
   for (int dt = 0; dt < DT; dt++) {
 #pragma unroll
     for (int r4 = 0; r4 < 4; r4++) {
-      // registers 4 r4 .. 4 r4 + 3 hold d .. d + 3 of this lane's query: one vector store
+      // registers 4 r4 .. 4 r4 + 3 hold d .. d + 3 of this lane's query
       const int d = dt * 32 + 8 * r4 + 4 * g;
       vec4_t v;
 #pragma unroll
       for (int e = 0; e < 4; e++) v[e] = (T)(o[dt][4 * r4 + e] * inv);
-      *reinterpret_cast<vec4_t *>(out + d) = v;
+      *reinterpret_cast<vec4_t *>(sO + ql * LDO + d) = v;
     }
+  }
+  __syncthreads();
+  // rows of queries past the sequence (clamped lanes) stay in LDS
+  const int rows = n - q0 < QT ? n - q0 : QT;
+  T *out = (T *)a.ctx + base * (int64_t)H * D + h * D;
+  for (int c = t; c < rows * CPR; c += 128) {
+    const int r = c / CPR, dc = (c % CPR) * CE;
+    *reinterpret_cast<uint4 *>(out + (int64_t)(q0 + r) * H * D + dc) = *reinterpret_cast<const uint4 *>(sO + r * LDO + dc);
   }
 }
 

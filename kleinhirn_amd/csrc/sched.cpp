@@ -64,9 +64,9 @@ int kh_sched_create(kh_plan *const *plans, int32_t n, kh_sched **out) {
         delete s;
         throw Fail(rc, kh_last_error());
       }
-      if (info.out_rows != info.batch) {
+      if (info.out_rows != info.batch || info.markers > 0) {
         delete s;
-        throw Fail(KH_EUNSUPPORTED, "the scheduler runs pooled heads (one output row per sequence)");
+        throw Fail(KH_EUNSUPPORTED, "the scheduler runs pooled heads (one output row per sequence, no markers)");
       }
       if (i > 0 && info.out_cols != s->cols) {
         delete s;

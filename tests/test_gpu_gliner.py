@@ -132,3 +132,22 @@ def test_marker_payloads_replace_and_reject():
         pooled.destroy()
     finally:
         be.dispose()
+
+
+def test_scheduler_rejects_marker_plans():
+    """kh_sched runs pooled heads only: a GLiNER2 plan of one marker slot (one output row per
+    sequence) is refused, since the scheduler uploads no marker payloads."""
+    import ctypes
+    from kleinhirn_amd.backend import HipBackend, lib
+    c, W, _, _ = reference()
+    be = HipBackend(configs.storage(W, True))
+    try:
+        r = be.runner(build_plan(c.spec, G.HEAD, G.LENGTH, 2, True, markers=1))
+        assert r.info.out_rows == 2
+        handles = (ctypes.c_void_p * 1)(r.h.value)
+        h = ctypes.c_void_p()
+        assert lib().kh_sched_create(handles, 1, ctypes.byref(h)) == 2  # KH_EUNSUPPORTED
+        assert b"no markers" in lib().kh_last_error()
+        r.destroy()
+    finally:
+        be.dispose()
