@@ -75,10 +75,13 @@ attn_kernel(AttnArgs a, Packing p) {
   __shared__ __attribute__((aligned(16))) float sRel[REL ? 2 * 2 * 32 * RP : 1];  // [wave][c2p|p2c][32][RP]
   __shared__ int sBucket[REL ? REL_BUCKETS : 1];
 
-  const int2 tile = a.tiles[blockIdx.x];
-  const int b = tile.x, q0 = tile.y;
-  const int h = blockIdx.y;
+  // items (head, query tile), tiles fastest: the query tiles of one sequence and head run
+  // together on one XCD and find its K and V rows in that XCD's L2
   const int H = a.H;
+  const int item = xcd_tile(blockIdx.x, a.ntiles * H);
+  const int2 tile = a.tiles[item % a.ntiles];
+  const int b = tile.x, q0 = tile.y;
+  const int h = item / a.ntiles;
   const int64_t base = p.cu[b];
   const int n = p.cu[b + 1] - p.cu[b];
   const int64_t rs = (int64_t)3 * H * D;  // qkv row stride
@@ -350,7 +353,7 @@ attn_kernel(AttnArgs a, Packing p) {
 
 template <typename T, bool REL, bool WIN>
 void launch_w(const AttnArgs &a, const Packing &p, hipStream_t s) {
-  dim3 grid((unsigned)a.ntiles, (unsigned)a.H);
+  dim3 grid((unsigned)(a.ntiles * a.H));
   if (a.D == 64) launch((attn_kernel<T, 64, REL, WIN>), grid, dim3(128), 0, s, a, p);
   else launch((attn_kernel<T, 32, REL, WIN>), grid, dim3(128), 0, s, a, p);
 }

@@ -29,6 +29,15 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Work item of block b in a 1-D grid of nblk blocks: the dispatcher sends block b to XCD b % 8, so
+// each XCD gets a contiguous range of items (neighbouring items share operands in that XCD's L2).
+__device__ __forceinline__ int xcd_tile(int tile, int nblk) {
+  const int per = (nblk + 7) / 8;
+  const int x = tile % 8, i = tile / 8;
+  const int full = nblk - (per - 1) * 8;  // XCDs that hold `per` items (the rest hold per - 1)
+  return x < full ? x * per + i : full * per + (x - full) * (per - 1) + i;
+}
+
 // GELU by erf through Abramowitz-Stegun 7.1.26 (the reference's constants, src/wasm/plan.ts:99-107)
 __device__ __forceinline__ float gelu_as(float v) {
   float u = v * 0.7071067811865476f;

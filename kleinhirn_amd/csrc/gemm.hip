@@ -86,14 +86,6 @@ __device__ __forceinline__ float act_fn(float v) {
   else return v;
 }
 
-__device__ __forceinline__ int xcd_tile(int tile, int nblk) {
-  // block b runs on XCD b % 8; give each XCD a contiguous range of tiles
-  const int per = (nblk + 7) / 8;
-  const int x = tile % 8, i = tile / 8;
-  const int full = nblk - (per - 1) * 8;  // XCDs that hold `per` tiles (the rest hold per - 1)
-  return x < full ? x * per + i : full * per + (x - full) * (per - 1) + i;
-}
-
 template <typename T, int BM, int BN, int WM, int WN, int ACT, int FM, int FN>
 __device__ __forceinline__ void epilogue(const GemmArgs &g, float16v (&acc)[FM][FN], int m0, int n0, int wm,
                                          int wn, int lane, int z) {
