@@ -581,6 +581,103 @@ __device__ __forceinline__ rsrc_t panel_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// Lean epilogue, staging half: bias, activation and the f16 conversion of this wavefront's
+// accumulators, written row-major into `lds` (rows of BN values, 16-byte chunks rotated by the row).
+// acc[i][j][4 q + e] is row row0 + 32 i, column wn TN + 32 j + 8 q + 4 lg + e of the staged rows.
+template <int BN, int WN, int ACT, int EPI, int FM, int FN>
+__device__ __forceinline__ void lean_stage(const GemmArgs &g, float16v (&acc)[FM][FN], char *lds, int n0, int wn,
+                                           int lane, int row0) {
+  constexpr int TN = BN / WN, RB = BN * 2, CPR = BN / 8;
+  const int lg = lane >> 5;
+  const half_t *bias = (const half_t *)g.bias;
+#pragma unroll
+  for (int j = 0; j < FN; j++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int nl = wn * TN + j * 32 + 8 * q;
+      // bias column of these 4 values: the tile's columns, or for GeGLU the rows of W its two
+      // halves take (columns n0 / 2 + c of each half of the product)
+      int n = n0 + nl + 4 * lg;
+      if constexpr (EPI == EPI_GEGLU) n = (nl < BN / 2 ? (n0 >> 1) + nl : g.N / 2 + (n0 >> 1) + nl - BN / 2) + 4 * lg;
+      float b[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bias && n < g.N) {
+        const half4v bv = *reinterpret_cast<const half4v *>(bias + n);
+        b[0] = (float)bv[0]; b[1] = (float)bv[1]; b[2] = (float)bv[2]; b[3] = (float)bv[3];
+      }
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+        const int ml = row0 + i * 32;
+        half4v o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[e] = (half_t)act_fn<ACT>(acc[i][j][4 * q + e] + b[e]);
+        const int chunk = ((nl >> 3) + ml) % CPR;
+        *reinterpret_cast<half4v *>(lds + ml * RB + chunk * 16 + lg * 8) = o;
+      }
+    }
+}
+
+// Lean epilogue, store half: ROWS staged rows (row r is C row grow0 + r) leave as whole 16-byte
+// chunks, through the fused step of EPI; NT threads share the rows.
+template <int ROWS, int BN, int NW, int EPI>
+__device__ __forceinline__ void lean_store(const GemmArgs &g, const char *lds, int grow0, int n0) {
+  constexpr int RB = BN * 2, CPR = BN / 8, NT = 64 * NW;
+  half_t *C = (half_t *)g.c;
+  auto chunk_at = [&](int row, int cc) {
+    return *reinterpret_cast<const half8v *>(lds + row * RB + ((cc + row) % CPR) * 16);
+  };
+  if constexpr (EPI == EPI_GEGLU) {
+    // output columns n0 / 2 .. n0 / 2 + BN / 2 of C [M, N / 2]: gelu(a) * b, a and b as stored
+    constexpr int HC = CPR / 2;
+    const int I = g.N / 2;
+#pragma unroll
+    for (int q = threadIdx.x; q < ROWS * HC; q += NT) {
+      const int row = q / HC, cc = q % HC;
+      const int grow = grow0 + row, gcol = (n0 >> 1) + cc * 8;
+      if (grow < g.M && gcol < I) {
+        const half8v x = chunk_at(row, cc), y = chunk_at(row, cc + HC);
+        half8v o;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = (half_t)(gelu_as((float)x[e]) * (float)y[e]);
+        *reinterpret_cast<half8v *>(C + (int64_t)grow * g.ldc + gcol) = o;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = threadIdx.x; q < ROWS * CPR; q += NT) {
+      const int row = q / CPR, cc = q % CPR;
+      const int grow = grow0 + row, gcol = n0 + cc * 8;
+      if (grow < g.M && gcol < g.N) {
+        half8v x = chunk_at(row, cc);
+        half_t *dst = C + (int64_t)grow * g.ldc + gcol;
+        if constexpr (EPI == EPI_ROPE) {
+          // rotate-half on q and k: d < D / 2 pairs with d + D / 2 of the same head (tiles start
+          // at head boundaries); cos at table[pos][d], sin at table[pos][D + d]
+          if (gcol < g.rope_cols) {
+            const int D = g.rope_d, half = D >> 1;
+            const int d0 = gcol % D;
+            const bool lo = d0 < half;
+            const half8v y = chunk_at(row, lo ? cc + half / 8 : cc - half / 8);
+            const float *t = g.rope_table + (int64_t)g.row_pos[grow] * 2 * D + (lo ? d0 : d0 - half);
+            half8v o;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+              const float c = t[e], sn = t[D + e];
+              o[e] = lo ? (half_t)((float)x[e] * c - (float)y[e] * sn) : (half_t)((float)x[e] * c + (float)y[e] * sn);
+            }
+            x = o;
+          }
+        } else if constexpr (EPI == EPI_RESADD) {
+          // residual += product, in f32, rounded once (the add op on the stored product)
+          const half8v r = *reinterpret_cast<const half8v *>(dst);
+#pragma unroll
+          for (int e = 0; e < 8; e++) x[e] = (half_t)((float)r[e] + (float)x[e]);
+        }
+        *reinterpret_cast<half8v *>(dst) = x;
+      }
+    }
+  }
+}
+
 template <int BM, int BN, int WM, int WN, int ACT, int EPI, int STAGES>
 __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, int tiles_n) {
   constexpr int NW = WM * WN;
@@ -593,30 +690,35 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
   constexpr int STAGE = (BM + BN) * 128;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
 
-  const int tile = xcd_tile(blockIdx.x, tiles_m * tiles_n);
-  const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int lg = lane >> 5;
 
-  const int rows_a = min(BM, g.M - m0), rows_w = min(BN, g.N - n0);
-  const rsrc_t ra = panel_rsrc((const half_t *)g.a + (int64_t)m0 * g.lda, (uint32_t)(rows_a * g.lda * 2));
-  // GeGLU: the tile's columns are BN / 2 rows of each half of W (all of W in one resource)
-  const rsrc_t rw = EPI == EPI_GEGLU
-                        ? panel_rsrc(g.w, (uint32_t)((int64_t)g.N * g.ldw * 2))
-                        : panel_rsrc((const half_t *)g.w + (int64_t)n0 * g.ldw, (uint32_t)(rows_w * g.ldw * 2));
-  // load p of this wavefront fills 8-row group wave * P + p: lane l writes row l / 8, position l % 8
+  // the tile's origin and the buffer resources and offsets of its row panels
+  int m0, n0;
+  rsrc_t ra, rw;
   uint32_t voff[P];
+  auto setup = [&](int tile) {
+    m0 = (tile / tiles_n) * BM;
+    n0 = (tile % tiles_n) * BN;
+    const int rows_a = min(BM, g.M - m0), rows_w = min(BN, g.N - n0);
+    ra = panel_rsrc((const half_t *)g.a + (int64_t)m0 * g.lda, (uint32_t)(rows_a * g.lda * 2));
+    // GeGLU: the tile's columns are BN / 2 rows of each half of W (all of W in one resource)
+    rw = EPI == EPI_GEGLU ? panel_rsrc(g.w, (uint32_t)((int64_t)g.N * g.ldw * 2))
+                          : panel_rsrc((const half_t *)g.w + (int64_t)n0 * g.ldw, (uint32_t)(rows_w * g.ldw * 2));
+    // load p of this wavefront fills 8-row group wave * P + p: lane l writes row l / 8, position l % 8
 #pragma unroll
-  for (int p = 0; p < P; p++) {
-    const int r = (wave * P + p) * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ swz(r);
-    int wr = r - BM;
-    if constexpr (EPI == EPI_GEGLU)
-      wr = (n0 >> 1) + (wr < BN / 2 ? wr : g.N / 2 + wr - BN / 2);
-    voff[p] = r < BM ? (uint32_t)((r * g.lda + c * 8) * 2) : (uint32_t)((wr * g.ldw + c * 8) * 2);
-  }
+    for (int p = 0; p < P; p++) {
+      const int r = (wave * P + p) * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ swz(r);
+      int wr = r - BM;
+      if constexpr (EPI == EPI_GEGLU)
+        wr = (n0 >> 1) + (wr < BN / 2 ? wr : g.N / 2 + wr - BN / 2);
+      voff[p] = r < BM ? (uint32_t)((r * g.lda + c * 8) * 2) : (uint32_t)((wr * g.ldw + c * 8) * 2);
+    }
+  };
+  setup(xcd_tile(blockIdx.x, tiles_m * tiles_n));
   auto issue = [&](int stage, int k0) {
 #pragma unroll
     for (int p = 0; p < P; p++) {
@@ -731,85 +833,9 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
   // tile goes row-major into LDS (16-byte chunks of a row rotated by the row) and leaves as
   // whole 16-byte chunks
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  constexpr int RB = BN * 2, CPR = BN / 8;
-  const half_t *bias = (const half_t *)g.bias;
-#pragma unroll
-  for (int j = 0; j < FN; j++)
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const int nl = wn * TN + j * 32 + 8 * q;
-      const int n = n0 + nl + 4 * lg;
-      float b[4] = {0.f, 0.f, 0.f, 0.f};
-      if (bias && n < g.N) {
-        const half4v bv = *reinterpret_cast<const half4v *>(bias + n);
-        b[0] = (float)bv[0]; b[1] = (float)bv[1]; b[2] = (float)bv[2]; b[3] = (float)bv[3];
-      }
-#pragma unroll
-      for (int i = 0; i < FM; i++) {
-        const int ml = arow + i * 32;
-        half4v o;
-#pragma unroll
-        for (int e = 0; e < 4; e++) o[e] = (half_t)act_fn<ACT>(acc[i][j][4 * q + e] + b[e]);
-        const int chunk = ((nl >> 3) + ml) % CPR;
-        *reinterpret_cast<half4v *>(smem + ml * RB + chunk * 16 + lg * 8) = o;
-      }
-    }
+  lean_stage<BN, WN, ACT, EPI>(g, acc, smem, n0, wn, lane, arow);
   __syncthreads();
-  half_t *C = (half_t *)g.c;
-  auto chunk_at = [&](int row, int cc) {
-    return *reinterpret_cast<const half8v *>(smem + row * RB + ((cc + row) % CPR) * 16);
-  };
-  if constexpr (EPI == EPI_GEGLU) {
-    // output columns n0 / 2 .. n0 / 2 + BN / 2 of C [M, N / 2]: gelu(a) * b, a and b as stored
-    constexpr int HC = CPR / 2;
-    const int I = g.N / 2;
-#pragma unroll
-    for (int q = threadIdx.x; q < BM * HC; q += 64 * NW) {
-      const int row = q / HC, cc = q % HC;
-      const int grow = m0 + row, gcol = (n0 >> 1) + cc * 8;
-      if (grow < g.M && gcol < I) {
-        const half8v x = chunk_at(row, cc), y = chunk_at(row, cc + HC);
-        half8v o;
-#pragma unroll
-        for (int e = 0; e < 8; e++) o[e] = (half_t)(gelu_as((float)x[e]) * (float)y[e]);
-        *reinterpret_cast<half8v *>(C + (int64_t)grow * g.ldc + gcol) = o;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int q = threadIdx.x; q < BM * CPR; q += 64 * NW) {
-      const int row = q / CPR, cc = q % CPR;
-      const int grow = m0 + row, gcol = n0 + cc * 8;
-      if (grow < g.M && gcol < g.N) {
-        half8v x = chunk_at(row, cc);
-        half_t *dst = C + (int64_t)grow * g.ldc + gcol;
-        if constexpr (EPI == EPI_ROPE) {
-          // rotate-half on q and k: d < D / 2 pairs with d + D / 2 of the same head (tiles start
-          // at head boundaries); cos at table[pos][d], sin at table[pos][D + d]
-          if (gcol < g.rope_cols) {
-            const int D = g.rope_d, half = D >> 1;
-            const int d0 = gcol % D;
-            const bool lo = d0 < half;
-            const half8v y = chunk_at(row, lo ? cc + half / 8 : cc - half / 8);
-            const float *t = g.rope_table + (int64_t)g.row_pos[grow] * 2 * D + (lo ? d0 : d0 - half);
-            half8v o;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-              const float c = t[e], sn = t[D + e];
-              o[e] = lo ? (half_t)((float)x[e] * c - (float)y[e] * sn) : (half_t)((float)x[e] * c + (float)y[e] * sn);
-            }
-            x = o;
-          }
-        } else if constexpr (EPI == EPI_RESADD) {
-          // residual += product, in f32, rounded once (the add op on the stored product)
-          const half8v r = *reinterpret_cast<const half8v *>(dst);
-#pragma unroll
-          for (int e = 0; e < 8; e++) x[e] = (half_t)((float)r[e] + (float)x[e]);
-        }
-        *reinterpret_cast<half8v *>(dst) = x;
-      }
-    }
-  }
+  lean_store<BM, BN, NW, EPI>(g, smem, m0, n0);
 }
 
 // (the body is a device function: the buffer-resource type exists only in device compilation)

@@ -132,6 +132,22 @@ def test_fused_product_steps_match_separate_ops(monkeypatch):
     assert cosine_rows(ref, fused).min() >= 0.999
 
 
+def test_fused_products_with_biases_match_separate_ops(monkeypatch):
+    """A ModernBERT with attention and MLP biases (spec bias=True): the fused GeGLU epilogue takes
+    each half's bias from that half's rows of the FFN-in product, as the separate product does."""
+    from kleinhirn_amd.plan import spec as S
+    from tests.helpers import Case
+    base, _ = case_and_oracle("c4")
+    spec = S.modernbert(384, 2, 6, 576, 50368, bias=True)
+    case = Case(spec, base.head, base.ids, base.length)
+    for name in ("layers.0.mlp_in.bias", "layers.0.wqkv.bias", "layers.1.attn_out.bias"):
+        assert np.abs(case.weights[name]).max() > 0, name  # seeded N(0, 0.02) biases, not zeros
+    fused = hip_outputs(case, f16=True)
+    monkeypatch.setenv("KH_NO_FUSION", "1")
+    separate = hip_outputs(case, f16=True)
+    assert np.array_equal(fused, separate), np.abs(fused - separate).max()
+
+
 @pytest.mark.parametrize("key", ["c2", "c3b", "c4", "c5"])
 def test_cls_tail_on_sequence_rows_equals_full_forward(monkeypatch, key):
     """A pooled-CLS head reads row 0 of each sequence after the last attention, so the runner runs
