@@ -198,9 +198,10 @@ int kh_upload_ids(kh_plan *plan, const int32_t *ids, size_t id_count, const floa
 
 /* The packedMarkers part of PlanRunner.upload (RunInput.packedMarkers, src/plan/executor.ts:28,
  * 385-388) for plans with a markers input (GLiNER2 span heads): per sequence 3 * markers u32, the
- * marker row indices, the marker mask as f32 bits and the group ids; count must be
- * 3 * markers * batch. Every row index must be below the plan length (KH_EINVAL at kh_run). Kept
- * until replaced; before the first call every slot is masked. A marker whose row lies past its
+ * marker row indices, the marker mask as f32 bits and the group ids; count up to
+ * 3 * markers * batch (a shorter payload replaces only the first count values, as the reference's
+ * upload does). Every row index must be below the plan length (KH_EINVAL at kh_run). Kept until
+ * replaced; before the first call every slot is masked. A marker whose row lies past its
  * sequence's valid rows gathers a zero state (the reference reads the padding row's state). */
 int kh_upload_markers(kh_plan *plan, const uint32_t *packed, size_t count);
 

@@ -1904,11 +1904,13 @@ int kh_upload_markers(kh_plan *plan, const uint32_t *packed, size_t count) {
   if (!plan) fail(KH_EINVAL, "null plan");
   require_live(plan->ctx);
   if (plan->in_markers.empty()) fail(KH_EINVAL, "the plan has no markers input");
+  // as the reference's upload puts the array at the buffer's start (src/plan/wasm.ts:411-416): a
+  // shorter payload leaves the later slots as they were, a longer one is an error
   const size_t want = (size_t)3 * plan->markers * plan->B;
-  if (!packed || count != want)
-    fail(KH_EINVAL, "packed markers hold " + std::to_string(count) + " u32, the plan takes 3 * " +
+  if ((count && !packed) || count > want)
+    fail(KH_EINVAL, "packed markers hold " + std::to_string(count) + " u32, the plan takes up to 3 * " +
                         std::to_string(plan->markers) + " * " + std::to_string(plan->B) + " = " + std::to_string(want));
-  memcpy(plan->markers_host.data(), packed, want * 4);
+  if (count) memcpy(plan->markers_host.data(), packed, count * 4);
   plan->dirty = true;  // the payload travels with the next run's packed metadata
   KH_API_END
 }

@@ -120,7 +120,13 @@ def test_marker_payloads_replace_and_reject():
         with pytest.raises(KhError, match="plan length"):
             r.run(G.LENGTH * B)
         with pytest.raises(KhError, match="packed markers"):
-            r._markers(np.concatenate(packed)[:-1])
+            r._markers(np.concatenate(packed + [packed[0][:1]]))
+        # a shorter payload replaces only its own values (the reference's put at offset 0)
+        r._markers(np.concatenate(packed))
+        r._markers(np.concatenate(moved)[:3 * K])
+        r.run(G.LENGTH * B)
+        short = r.read_output().reshape(B, -1)
+        assert np.array_equal(short, a)
         with pytest.raises(ValueError, match="packedMarkers"):
             r.upload({k: v for k, v in ri.items() if k != "packedMarkers"})
         r.destroy()
