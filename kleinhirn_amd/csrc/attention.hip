@@ -257,7 +257,7 @@ attn_kernel(AttnArgs a, Packing p) {
       if (REL || WIN || k0 + 32 > khi) scores(std::true_type{});
       else scores(std::false_type{});
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    tmax = fmaxf(tmax, xor32(tmax));
     const float m_new = fmaxf(m_run, tmax * scale2);
     // a query with no key so far keeps its state (corr 1, weights exp2(-inf) = 0)
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
@@ -319,7 +319,7 @@ attn_kernel(AttnArgs a, Packing p) {
     __syncthreads();
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = l_run + xor32(l_run);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   // The output tile leaves through LDS (the K tile's space, free after the key loop's last
   // barrier): a lane holds 4-value pieces of one query row, scattered over 32 rows per store;

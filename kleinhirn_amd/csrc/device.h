@@ -23,6 +23,15 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// v of lane ^ 32 (the other half of the wavefront). The lane id is read where the exchange runs
+// (a volatile asm the compiler does not hoist), so no index register stays live across the
+// caller's loops, and ds_bpermute needs no bounds handling for an in-wave partner.
+__device__ __forceinline__ float xor32(float v) {
+  int lane;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __float_as_int(v)));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
