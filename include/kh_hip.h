@@ -214,7 +214,7 @@ int kh_upload_qtypes(kh_plan *plan, const uint32_t *qtype, size_t count);
 
 /* PlanRunner.run (src/plan/executor.ts:295-297): one forward over `rows` rows (the real rows of
  * a B = 1 call, L * B for a batch plan), enqueued on the plan's stream; returns without waiting.
- * A batch call with fewer than KH_SPLIT_T (environment, default 65536) valid rows runs as two
+ * A batch call with fewer than KH_SPLIT_T (environment, default 400000) valid rows runs as two
  * halves of about equal rows on two streams (KH_NO_SPLIT=1: one stream); outputs are the same. */
 int kh_run(kh_plan *plan, int32_t rows);
 

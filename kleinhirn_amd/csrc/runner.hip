@@ -1168,7 +1168,9 @@ static int64_t env_int(const char *name, int64_t dflt) {
 
 // Sequences [0, split) stay on this plan; 0 runs the batch whole. Only batch calls (rows = L * B)
 // of plans whose output rows are per sequence or per token split, and only below KH_SPLIT_T valid
-// rows (default 65536: above that one half's grids already fill the chip), with both halves holding
+// rows (default 400000: a few hundred thousand rows of long sequences still leave the chip idle
+// in attention phases the other half fills; at a million rows the halves gain nothing), with both
+// halves holding
 // about half the rows.
 static int choose_split(const kh_plan *pl, int rows) {
   if (pl->is_twin || pl->B < 2 || rows != pl->L * pl->B || env_int("KH_NO_SPLIT", 0)) return 0;
@@ -1184,7 +1186,7 @@ static int choose_split(const kh_plan *pl, int rows) {
     pre[b + 1] = pre[b] + len;
   }
   const int64_t T = pre[pl->B];
-  if (T < env_int("KH_SPLIT_MIN", 2048) || T >= env_int("KH_SPLIT_T", 65536)) return 0;
+  if (T < env_int("KH_SPLIT_MIN", 2048) || T >= env_int("KH_SPLIT_T", 400000)) return 0;
   int split = 1;
   while (split < pl->B - 1 && 2 * pre[split] < T) split++;
   if (pre[split] == 0 || pre[split] == T) return 0;
@@ -1266,7 +1268,7 @@ static void stage_twin(kh_plan *pl, int split) {
 static void launch_forward(kh_plan *pl, int rows, const LaunchHook &hook, bool sequential) {
   // the split depends on the upload (dirty), the row count and the two switches
   const int64_t env =
-      (env_int("KH_NO_SPLIT", 0) * 1000003 + env_int("KH_SPLIT_T", 65536)) * 1000003 + env_int("KH_SPLIT_MIN", 2048);
+      (env_int("KH_NO_SPLIT", 0) * 1000003 + env_int("KH_SPLIT_T", 400000)) * 1000003 + env_int("KH_SPLIT_MIN", 2048);
   if (pl->dirty || pl->split_memo < 0 || rows != pl->split_memo_rows || env != pl->split_memo_env) {
     pl->split_memo = choose_split(pl, rows);
     pl->split_memo_rows = rows;
