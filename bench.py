@@ -5,7 +5,7 @@ over inputs already resident in HBM. The default workload is BASELINE.json's hea
 (RoBERTa-base shape, f16 storage / f32 accumulate, 256 sequences with lognormal lengths, median
 45, packed without padding); --workload picks another benchmark config.
 
-The timed steps run as the library runs them: a batch with fewer than 65,536 valid rows goes as two
+The timed steps run as the library runs them: a batch with fewer than 400,000 valid rows goes as two
 halves on two streams (`streams` in the line). After them the bench times, per launch, the same
 steps with the whole batch on one stream and a HIP event pair around every launch on that stream
 (kh_trace): events around each launch would serialise the two streams, so the split run cannot be
@@ -34,45 +34,127 @@ PEAK = {"f16_mfma_tflops": 2500.0, "f32_mfma_tflops": 157.3, "hbm_gbs": 8000.0}
 # FETCH_SIZE reads 0.5 GiB -> x2.0, WRITE_SIZE reads 1.0 GiB -> x1.0). Summaries with the commands:
 # profiles/gemm_mfma_c2_roberta_base_ragged256_traffic.md. Re-measured whenever the kernel changes.
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
-TRAFFIC_KIB = {  # (workload, family): (FETCH_SIZE KiB, WRITE_SIZE KiB) per dispatch
-    ("c2-roberta-base-f16-ragged256", "gemm_mfma"): (54097.1, 40025.3),
+TRAFFIC_KIB = {  # (workload, family): (FETCH_SIZE KiB, WRITE_SIZE KiB) per dispatch, kernel source sha256[:16]
+    ("c2-roberta-base-f16-ragged256", "gemm_mfma"): (54097.1, 40025.3, "9bbde0fd85b000a9"),
 }
+# the source file of each kernel family (a counter figure measured on other code is not reported)
+FAMILY_SOURCE = {"gemm_mfma": "gemm.hip", "attention": "attention.hip", "layernorm": "rowops.hip",
+                 "embln": "rowops.hip"}
+
+
+def source_digest(family: str) -> str | None:
+    import hashlib
+    f = FAMILY_SOURCE.get(family)
+    if not f:
+        return None
+    with open(os.path.join(ROOT, "kleinhirn_amd", "csrc", f), "rb") as fh:
+        return hashlib.sha256(fh.read()).hexdigest()[:16]
+
+
+def physical_cores(cpus) -> int:
+    """Distinct (package, core) pairs among the CPUs this process may run on."""
+    seen, cur = set(), {}
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh.read().split("\n") + [""]:
+                if not line.strip():
+                    if cur.get("processor") in cpus:
+                        seen.add((cur.get("physical id"), cur.get("core id")))
+                    cur = {}
+                    continue
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                cur[k] = int(v) if k == "processor" else v
+    except OSError:
+        return len(cpus)
+    return len(seen) or len(cpus)
+
+
+def run_facts() -> dict:
+    """BASELINE.md section 7's record fields: commit, ROCm version, device name and clock."""
+    import ctypes
+    facts = {}
+    try:
+        with open(os.path.join(ROOT, "kleinhirn_amd", "build_info.json")) as fh:
+            facts.update(json.load(fh))
+    except (OSError, ValueError):
+        facts["commit"] = None
+    try:
+        with open("/opt/rocm/.info/version") as fh:
+            facts["rocm"] = fh.read().strip()
+    except OSError:
+        facts["rocm"] = None
+    try:
+        import torch
+        props = torch.cuda.get_device_properties(0)
+        facts["device"] = f"{props.name} ({getattr(props, 'gcnArchName', '?')}, {props.multi_processor_count} CUs)"
+        hip = ctypes.CDLL("libamdhip64.so")
+        v = ctypes.c_int(0)
+        if hip.hipDeviceGetAttribute(ctypes.byref(v), 5, 0) == 0:  # hipDeviceAttributeClockRate (kHz, peak)
+            facts["clock_mhz"] = v.value // 1000
+    except Exception:
+        pass
+    return facts
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(w, weights, seconds: float = 12.0) -> dict:
+def cpu_baseline(w, weights, seconds: float = 12.0, threads: int | None = None) -> tuple[dict, np.ndarray]:
     """The oracle on the host cores, the reference's WASM schedule (one sequence at a time on the
-    bucket plan, real rows only), threads = min(cores, 8) as the reference's 'auto'
-    (src/wasm-plan-host.ts:35-49), over as many sequences of the batch as fit ~`seconds`."""
+    bucket plan, real rows only), over as many sequences of the batch as fit ~`seconds`; threads
+    default to min(cores, 8), the reference's 'auto' (src/wasm-plan-host.ts:35-49). Returns the
+    figure and the oracle's outputs for the sequences it ran (the parity check's reference)."""
     from kleinhirn_amd import inputs
     from kleinhirn_amd.plan.build import build_plan
     from oracle.oracle import OracleRuntime
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    threads = max(1, min(cores or 1, 8))
+    cpus = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    phys = physical_cores(set(cpus))
+    threads = threads or max(1, min(len(cpus), 8))
     plan = build_plan(w.spec, w.head, w.length, 1, False)
     rt = OracleRuntime(weights, [plan])
     p = rt.plan(plan, threads=threads)
     table = weights["embeddings.word.weight"]
     ids = w.ids()
     done = toks = 0
+    outs = []
     t0 = time.perf_counter()
     for seq in ids:
         ri = inputs.run_input(w.spec, table, [seq], w.length)
         p.upload(ri["embeddings"], ri["mask"], ri["typeIds"])
         p.run(len(seq))
-        p.read_output()
+        outs.append(p.read_output())
         done += 1
         toks += len(seq)
         if time.perf_counter() - t0 > seconds:
             break
     dt = time.perf_counter() - t0
-    return {"value": round(done / dt, 3), "unit": "sequences/s", "cores": threads, "kind": "port",
-            "tokens_per_s": round(toks / dt, 1),
-            "sample": f"first {done} of {len(ids)} sequences ({toks} tokens), one B=1 bucket plan "
-                      f"(L={w.length}) per sequence, f32, {threads} OpenMP threads of {cores} cores"}
+    fig = {"value": round(done / dt, 3), "unit": "sequences/s", "cores": threads, "kind": "port",
+           "tokens_per_s": round(toks / dt, 1),
+           "sample": f"first {done} of {len(ids)} sequences ({toks} tokens), one B=1 bucket plan "
+                     f"(L={w.length}) per sequence, f32, {threads} OpenMP threads; the process may run on "
+                     f"{len(cpus)} CPUs ({phys} physical cores)"}
+    return fig, np.stack(outs)
+
+
+def parity(ref: np.ndarray, got: np.ndarray, embedding: bool) -> dict:
+    """The reference's whole-run gate (bench/kbench/runner-lib.mjs:171-195,
+    convert/k28_close_calls.py:1-8): largest logit deviation, decisions that agree, decisions
+    excluded because their f32 top-2 gap is under twice that deviation, exact argmax identity, and
+    the smallest row cosine."""
+    ref = ref.astype(np.float64)
+    got = got.astype(np.float64)
+    delta = float(np.abs(ref - got).max())
+    cos = (ref * got).sum(1) / np.maximum(np.linalg.norm(ref, axis=1) * np.linalg.norm(got, axis=1), 1e-30)
+    out = {"n": int(len(ref)), "max_dlogit": round(delta, 6), "min_cosine": round(float(cos.min()), 6)}
+    if ref.shape[1] > 1 and not embedding:
+        top2 = np.sort(ref, axis=1)[:, -2:]
+        flippable = (top2[:, 1] - top2[:, 0]) < 2 * delta
+        same = ref.argmax(1) == got.argmax(1)
+        out.update(agree=int((same | flippable).sum()), excluded=int(flippable.sum()),
+                   identical=int(same.sum()), mismatched=int((~same & ~flippable).sum()))
+    return out
 
 
 def main() -> int:
@@ -93,7 +175,7 @@ def main() -> int:
         return 2
 
     import torch  # device plumbing only: the hot path is libkh_hip.so
-    from kleinhirn_amd import configs, inputs
+    from kleinhirn_amd import configs, inputs, synth
     from kleinhirn_amd.backend import HipBackend
     from kleinhirn_amd.plan.build import build_plan
 
@@ -118,13 +200,15 @@ def main() -> int:
             flat[b * w.length:b * w.length + len(seq)] = seq
         r.upload_ids(flat, mask, tt)
     else:
-        r.upload(inputs.run_input(w.spec, W["embeddings.word.weight"], ids, w.length))
+        run_input = inputs.run_input(w.spec, W["embeddings.word.weight"], ids, w.length)
+        r.upload(run_input)
     # boundary time of the first call: packing + H2D of the valid rows + forward + readback
     t0 = time.perf_counter()
     r.run(rows)
     out = r.read_output()
     boundary_ms = (time.perf_counter() - t0) * 1e3
     assert np.isfinite(out).all()
+    out = out.reshape(w.batch, -1)
     T = r.packed_rows()
     for _ in range(args.warmup):
         r.run(rows)
@@ -139,6 +223,19 @@ def main() -> int:
     streams = int(r.info.streams)
     seq_s = w.batch / dt
     tok_s = T / dt
+    # steady-state boundary: host RunInput -> upload -> run -> host f32 output, one call after the other
+    bts = []
+    for _ in range(max(3, min(10, args.steps))):
+        t0 = time.perf_counter()
+        if args.ids:
+            r.upload_ids(flat, mask, tt)
+        else:
+            r.upload(run_input)
+        r.run(rows)
+        r.read_output()
+        bts.append(time.perf_counter() - t0)
+    bts.sort()
+    bdt = bts[len(bts) // 2]
     if args.no_trace:
         print(json.dumps({"metric": "sequences/sec", "value": round(seq_s, 1), "ms_per_step": round(dt * 1e3, 4),
                           "streams": streams}), flush=True)
@@ -191,17 +288,38 @@ def main() -> int:
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK["hbm_gbs"], "unit": "GB/s"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
     kib = TRAFFIC_KIB.get((w.name, dom_name))
-    roof["traffic"] = round((kib[0] * FETCH_SCALE + kib[1] * WRITE_SCALE) * 1024) if kib else None
+    # a counter figure holds only for the kernel source it was measured on
+    current = kib is not None and kib[2] == source_digest(dom_name)
+    roof["traffic"] = round((kib[0] * FETCH_SCALE + kib[1] * WRITE_SCALE) * 1024) if current else None
     roof["traffic_unit"] = "bytes/launch (rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE, copy-calibrated)"
+    if kib is not None and not current:
+        roof["traffic_note"] = "counters measured on another revision of the kernel source: not reported"
     roof["algorithmic_bytes"] = round(dom["bytes"] / dom["launches"])
     roof["kernel"] = dom_name
     roof["avg_launch_ms"] = round(avg_ms, 4)
     roof["launches"] = int(round(dom["launches"]))  # per step
     roof["mode"] = "per launch: the timed steps re-run with the whole batch on one stream, HIP events around each launch"
 
-    cpu = None
+    cpu = cpu_all = None
+    checks = []
+    embedding = w.head.get("type") == "embed"
     if not args.no_cpu:
-        cpu = cpu_baseline(w, weights, args.cpu_seconds)
+        cpu, ref = cpu_baseline(w, weights, args.cpu_seconds)
+        checks.append(dict(parity(ref, out[:len(ref)], embedding), reference="oracle on this host, the CPU sample"))
+        cpus = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else [0]
+        allc = physical_cores(set(cpus))
+        if allc != cpu["cores"]:
+            cpu_all, _ = cpu_baseline(w, weights, args.cpu_seconds, threads=allc)
+    # the whole batch against the committed oracle outputs of the same seeded batch
+    gold = os.path.join(ROOT, "tests", "golden", f"oracle_{args.workload}_full.npz")
+    if os.path.exists(gold):
+        import hashlib
+        g = np.load(gold)
+        n = len(g["out"])
+        ids_ok = hashlib.sha256(np.concatenate(ids[:n]).astype(np.int32).tobytes()).hexdigest() == str(g["ids_sha256"])
+        if ids_ok and np.array_equal(np.array([len(x) for x in ids[:n]]), g["lengths"]):
+            checks.append(dict(parity(g["out"], out[:n], embedding),
+                               reference="committed oracle outputs (tests/golden) of the same sequences"))
 
     line = {
         "metric": "sequences/sec + tokens/sec, BERT-base f16 ragged batch; % MFMA / HBM peak",
@@ -214,8 +332,15 @@ def main() -> int:
                    "word_rows": "device gather" if args.ids else "host gather, uploaded once"},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "cpu_baseline_all_cores": cpu_all,
+        "parity": checks,
         "gpu_kernel_ms": round(total_ms, 4), "streams": streams,
         "first_call_boundary_ms": round(boundary_ms, 2),
+        "boundary": {"value": round(w.batch / bdt, 1), "unit": "sequences/s", "ms_per_call": round(bdt * 1e3, 3),
+                     "mode": "host RunInput -> kh_upload -> kh_run -> kh_read_output (f32), calls back to back, "
+                             "median"},
+        "seed": synth.SEED,
+        **run_facts(),
     }
     print(json.dumps(line), flush=True)
     r.destroy()

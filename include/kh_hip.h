@@ -254,6 +254,13 @@ int kh_trace_read(kh_plan *plan, kh_launch_stat *out, int32_t cap, int32_t *coun
 /* Packed rows (sum of valid sequence lengths) of the last run. */
 int kh_packed_rows(const kh_plan *plan, int64_t *out);
 
+/* Raw bytes of a plan buffer as the last run left them (storage dtype, packed rows first): waits
+ * for the plan's stream, copies min(bytes, buffer size) bytes. `half` 1 reads the buffer of the
+ * second half of a split batch (the twin plan). Replaces the buffer reads of the reference's
+ * capture tool (PlanRunner.readCapture, src/plan/executor.ts:177-195), for the layer-by-layer
+ * comparisons of a debugging session; KH_EINVAL for a buffer without device memory. */
+int kh_plan_read_buffer(kh_plan *plan, const char *id, int32_t half, void *out, size_t bytes);
+
 int kh_plan_destroy(kh_plan *plan);
 
 #ifdef __cplusplus

@@ -30,7 +30,7 @@ EXPORTS = [
     "kh_plan_info_get", "kh_upload", "kh_upload_ids", "kh_upload_markers", "kh_upload_qtypes", "kh_run", "kh_read_output", "kh_sync",
     "kh_last_run_ms", "kh_profile", "kh_packed_rows", "kh_plan_destroy", "kh_manifest_check",
     "kh_load_manifest", "kh_sha256", "kh_row_checksum", "kh_scores", "kh_read_scores", "kh_rank",
-    "kh_sched_create", "kh_sched_run", "kh_sched_destroy", "kh_trace", "kh_trace_read",
+    "kh_sched_create", "kh_sched_run", "kh_sched_destroy", "kh_trace", "kh_trace_read", "kh_plan_read_buffer",
 ]
 
 # kh_scores kinds
@@ -110,6 +110,7 @@ def lib() -> ctypes.CDLL:
         "kh_last_run_ms": [vp, ctypes.POINTER(ctypes.c_float)],
         "kh_profile": [vp, i32, ctypes.POINTER(LaunchStat), i32, ctypes.POINTER(i32)],
         "kh_packed_rows": [vp, ctypes.POINTER(i64)],
+        "kh_plan_read_buffer": [vp, ctypes.c_char_p, i32, vp, sz],
         "kh_plan_destroy": [vp],
         "kh_manifest_check": [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ManifestInfo)],
         "kh_load_manifest": [vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ManifestInfo)],
@@ -296,6 +297,13 @@ class HipPlanRunner:
         n = ctypes.c_int64()
         _check(lib().kh_packed_rows(self.h, ctypes.byref(n)))
         return int(n.value)
+
+    def read_buffer(self, bid: str, nbytes: int, half: int = 0) -> np.ndarray:
+        """Raw bytes of plan buffer `bid` after the last run (`half` 1: the second half of a split
+        batch), as uint8 (kh_plan_read_buffer)."""
+        out = np.zeros(nbytes, dtype=np.uint8)
+        _check(lib().kh_plan_read_buffer(self.h, bid.encode(), int(half), out.ctypes.data, out.nbytes))
+        return out
 
     def profile(self, rows: int) -> list[dict]:
         cap = 4096

@@ -49,7 +49,25 @@ def build(verbose: bool = False) -> str:
     subprocess.run([HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", *objs, "-o", tmp], check=True)
     os.replace(tmp, LIB)
     build_addon()
+    write_build_info()
     return LIB
+
+
+def write_build_info() -> None:
+    """kleinhirn_amd/build_info.json: the commit the library was built from (and whether the tree
+    held uncommitted changes), read by bench.py where the tree has no git history."""
+    import json
+    info = {"commit": None, "dirty": None}
+    try:
+        info["commit"] = subprocess.run(["git", "-C", ROOT, "rev-parse", "--short=12", "HEAD"], capture_output=True,
+                                        text=True, check=True).stdout.strip()
+        st = subprocess.run(["git", "-C", ROOT, "status", "--porcelain", "--untracked-files=no"],
+                            capture_output=True, text=True, check=True).stdout
+        info["dirty"] = bool(st.strip())
+    except (OSError, subprocess.CalledProcessError):
+        pass
+    with open(os.path.join(HERE, "build_info.json"), "w") as fh:
+        json.dump(info, fh)
 
 
 ADDON = os.path.join(HERE, "node", "kh_addon.node")

@@ -123,7 +123,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmArgs &g, float16v (&acc)[
   constexpr int RB = BN * 2;  // bytes per LDS row
   const int lg = lane >> 5;
   const half_t *bias = (const half_t *)g.bias;
-  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // the ring is no longer read
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");  // the ring is no longer read
 #pragma unroll
   for (int j = 0; j < FN; j++) {
     const int c = wn * TN + j * 32 + (lane & 31);
@@ -237,10 +237,14 @@ gemm_dma_kernel(GemmArgs g, int tiles_m, int tiles_n) {
     // Slab `it` complete for this wavefront (later slabs may stay in flight), then a barrier: every
     // wavefront's part of slab `it` landed and slab it-1 is no longer read. Written as one asm
     // block: __syncthreads() would add a release fence, i.e. a wait for every outstanding load.
+    // lgkmcnt(0): this wavefront's own LDS reads are complete before it signals the barrier. The
+    // scheduler may sink the last MFMAs of a slab, and the waits for their operands, below the
+    // asm; a read still in flight there could return the next issue's data (seen with two streams
+    // loading a CU's LDS, where a read can be delayed by hundreds of cycles).
     if (it + STAGES - 2 < nk) {
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((STAGES - 2) * P) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((STAGES - 2) * P) : "memory");
     } else {
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
     if (it + STAGES - 1 < nk) issue((it + STAGES - 1) % STAGES, (it + STAGES - 1) * BK);
     const char *slab = smem + (it % STAGES) * STAGE;
@@ -367,9 +371,9 @@ gemm_persist_kernel(GemmArgs g, int tiles_m, int tiles_n) {
 
   for (int q = 0; q < total; q++) {
     if (q + STAGES - 2 < total) {
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((STAGES - 2) * P) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((STAGES - 2) * P) : "memory");
     } else {
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
     if (q + STAGES - 1 < total) issue(q + STAGES - 1);
     const char *slab = smem + (q % STAGES) * STAGE;
@@ -790,23 +794,25 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
   };
 
   if constexpr (STAGES == 2) {
-    // slab s in stage s % 2: wait for this wavefront's loads of s, then a barrier (every part
-    // landed, and the stage the next issue overwrites is no longer read). The first slab is peeled
+    // slab s in stage s % 2: wait for this wavefront's loads of s and for its own LDS reads, then a
+    // barrier (every part landed, and the stage the next issue overwrites is no longer read by a
+    // read still in flight; the compiler may sink the last MFMAs and their operand waits below the
+    // asm, so the reads must be waited here). The first slab is peeled
     // and the loop body holds two whole slabs, so the accumulators stay in place across iterations.
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (1 < nk) issue(1, 64);
     slab(smem, std::true_type{});
     int it = 1;
     for (; it + 1 < nk; it += 2) {
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
       issue(0, (it + 1) * 64);
       slab(smem + STAGE, std::false_type{});
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
       if (it + 2 < nk) issue(1, (it + 2) * 64);
       slab(smem, std::false_type{});
     }
     if (it < nk) {
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
       slab(smem + STAGE, std::false_type{});
     }
   } else {
@@ -816,8 +822,8 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
     static_assert((STAGES - 2) * P <= 63, "vmcnt counts up to 63 loads");
     for (int i = 1; i < STAGES - 1 && i < nk; i++) issue(i, i * 64);
     auto wait_for = [&](int sl) {
-      if (sl + STAGES - 2 < nk) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((STAGES - 2) * P) : "memory");
-      else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      if (sl + STAGES - 2 < nk) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((STAGES - 2) * P) : "memory");
+      else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     };
     wait_for(0);
     if (STAGES - 1 < nk) issue(STAGES - 1, (STAGES - 1) * 64);
@@ -832,7 +838,7 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
   // epilogue: acc[i][j][4 q + e] is C[m0 + arow + 32 i][n0 + wn TN + 32 j + 8 q + 4 lg + e]; the
   // tile goes row-major into LDS (16-byte chunks of a row rotated by the row) and leaves as
   // whole 16-byte chunks
-  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   lean_stage<BN, WN, ACT, EPI>(g, acc, smem, n0, wn, lane, arow);
   __syncthreads();
   lean_store<BM, BN, NW, EPI>(g, smem, m0, n0);

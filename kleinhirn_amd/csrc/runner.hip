@@ -161,6 +161,7 @@ struct Buffer {
   bool packed_space = false;
   std::unique_ptr<DevMem> mem;
   std::vector<uint8_t> init;
+  bool init_done = false;  // init holds what the device buffer (or the relidx bucket table) holds
 };
 
 static const std::set<std::string> kMatmul = {"matmul", "mmtile", "mmtile8", "mmtile16"};
@@ -204,6 +205,7 @@ struct kh_plan {
   std::vector<std::pair<std::string, std::vector<uint8_t>>> init_log;  // kh_plan_init_buffer calls
   kh_plan *twin = nullptr;
   bool is_twin = false;
+  bool twin_failed = false;  // the twin could not be allocated: every batch runs whole
   int split = 0;
   hipEvent_t ev_twin = nullptr;
   // choose_split's answer for the current upload, row count and switches (-1: not computed)
@@ -216,7 +218,8 @@ struct kh_plan {
   std::vector<hipEvent_t> ev_pool;
 
   // upload staging (host, padded layout as the caller gave it)
-  std::vector<uint8_t> emb_host;
+  std::vector<uint8_t> emb_host;  // padded [L * B, E] layout; only the valid rows are filled
+  size_t emb_valid = 0;           // bytes the caller's array held (rows past it were not given)
   std::vector<float> mask_host;
   std::vector<uint32_t> tt_host;
   std::vector<int32_t> ids_host;
@@ -1106,7 +1109,7 @@ static void pack(kh_plan *pl, int rows, int b_end) {
     for (int b = 0; b < B; b++) {
       const size_t src = (size_t)b * L * row;
       const size_t nb = (size_t)n[b] * row;
-      if (src + nb > pl->emb_host.size()) fail(KH_EINVAL, "word rows shorter than the mask's valid rows");
+      if (src + nb > pl->emb_valid) fail(KH_EINVAL, "word rows shorter than the mask's valid rows");
       memcpy(dst + (size_t)pl->cu[b] * row, pl->emb_host.data() + src, nb);
     }
     if ((size_t)T * row > eb.mem->bytes) fail(KH_EINVAL, "packed rows exceed the emb buffer");
@@ -1135,7 +1138,13 @@ static void init_buffer(kh_plan *plan, const char *id, const void *data, size_t 
   if (it == plan->bufs.end()) fail(KH_EINVAL, std::string("plan buffer ") + id + " missing");
   Buffer &b = it->second;
   if ((int64_t)bytes > b.bytes) fail(KH_EINVAL, std::string("init of ") + id + " larger than the buffer");
+  // an unchanged table needs no device write (the twin's shifted CLS markers on every upload)
+  if (b.init.size() == bytes && (bytes == 0 || memcmp(b.init.data(), data, bytes) == 0) && b.init_done) return;
+  // kernels already queued on the plan's stream may read the table being replaced: the copies
+  // below are synchronous and unordered with that stream, so they wait for it first
+  if (plan->stream) KH_CHECK(hipStreamSynchronize(plan->stream));
   b.init.assign((const uint8_t *)data, (const uint8_t *)data + bytes);
+  b.init_done = true;
   const std::string sid = id;
   if (sid == "relidx") {
     // relidx[i][j] depends on i - j only: keep bucket(i - j) for i - j in [-(L-1), L-1]
@@ -1173,7 +1182,7 @@ static int64_t env_int(const char *name, int64_t dflt) {
 // halves holding
 // about half the rows.
 static int choose_split(const kh_plan *pl, int rows) {
-  if (pl->is_twin || pl->B < 2 || rows != pl->L * pl->B || env_int("KH_NO_SPLIT", 0)) return 0;
+  if (pl->is_twin || pl->twin_failed || pl->B < 2 || rows != pl->L * pl->B || env_int("KH_NO_SPLIT", 0)) return 0;
   if (!pl->in_markers.empty()) return 0;  // marker heads run whole
   const bool per_seq = !pl->out_packed && pl->out_rows == pl->B;
   const bool per_tok = pl->out_packed && pl->out_rows == pl->L * pl->B;
@@ -1193,8 +1202,21 @@ static int choose_split(const kh_plan *pl, int rows) {
   return split;
 }
 
+// device bytes of the plan's activation buffers (what a twin allocates again)
+static int64_t plan_buffer_bytes(const kh_plan *pl) {
+  int64_t n = 0;
+  for (const auto &b : pl->bufs)
+    if (b.second.mem) n += (int64_t)b.second.mem->bytes;
+  return n;
+}
+
+// KH_ENOMEM when the twin cannot be allocated (KH_TWIN_MAX_BYTES caps its buffers, for tests of
+// this path); the caller then runs the batch whole
 static void ensure_twin(kh_plan *pl) {
   if (pl->twin) return;
+  const int64_t cap = env_int("KH_TWIN_MAX_BYTES", -1);
+  if (cap >= 0 && plan_buffer_bytes(pl) > cap)
+    fail(KH_ENOMEM, "twin plan: " + std::to_string(plan_buffer_bytes(pl)) + " bytes of buffers over KH_TWIN_MAX_BYTES");
   kh_plan *t = nullptr;
   int rc = kh_plan_create(pl->ctx, pl->json.data(), pl->json.size(), &t);
   if (rc) fail(rc, std::string("twin plan: ") + kh_last_error());
@@ -1251,12 +1273,13 @@ static void stage_twin(kh_plan *pl, int split) {
     // only the valid rows of each moved sequence (pack reads no others): about T / 2 rows
     const size_t row = (size_t)pl->E * (pl->f16 ? 2 : 4);
     if (t->emb_host.size() != M * row) t->emb_host.resize(M * row);
+    t->emb_valid = t->emb_host.size();
     for (int b = split; b < pl->B; b++) {
       const float *m = pl->mask_host.data() + (size_t)b * L;
       size_t len = 0;
       while (len < L && m[len] > 0.5f) len++;
       const size_t src = (size_t)b * L * row, dst = (size_t)(b - split) * L * row;
-      if (src + len * row > pl->emb_host.size()) fail(KH_EINVAL, "word rows shorter than the mask's valid rows");
+      if (src + len * row > pl->emb_valid) fail(KH_EINVAL, "word rows shorter than the mask's valid rows");
       if (len) memcpy(t->emb_host.data() + dst, pl->emb_host.data() + src, len * row);
     }
   }
@@ -1274,11 +1297,19 @@ static void launch_forward(kh_plan *pl, int rows, const LaunchHook &hook, bool s
     pl->split_memo_rows = rows;
     pl->split_memo_env = env;
   }
-  const int split = pl->split_memo;
-  if (split > 0) {
-    ensure_twin(pl);
-    if (pl->dirty || split != pl->split) stage_twin(pl, split);
+  int split = pl->split_memo;
+  if (split > 0 && !pl->twin) {
+    try {
+      ensure_twin(pl);
+    } catch (const Error &e) {
+      if (e.code != KH_ENOMEM) throw;
+      // out of device memory for the second half's buffers: this plan runs whole from now on
+      (void)hipGetLastError();
+      pl->twin_failed = true;
+      pl->split_memo = split = 0;
+    }
   }
+  if (split > 0 && (pl->dirty || split != pl->split)) stage_twin(pl, split);
   if (pl->dirty || rows != pl->last_rows || split != pl->split) pack(pl, rows, split > 0 ? split : pl->B);
   pl->split = split;
   ensure_rel(pl);
@@ -1291,6 +1322,9 @@ static void launch_forward(kh_plan *pl, int rows, const LaunchHook &hook, bool s
   run_steps(pl, hook);
   if (split > 0) {
     if (sequential) KH_CHECK(hipStreamSynchronize(pl->stream));  // profiled halves one after the other
+    // the twin's half starts with this call, not when the twin finished the previous call's half
+    // (ev0 follows everything queued before on the plan's stream, the previous call's end included)
+    KH_CHECK(hipStreamWaitEvent(t->stream, pl->ev0, 0));
     run_steps(t, hook);
     KH_CHECK(hipEventRecord(pl->ev_twin, t->stream));
     KH_CHECK(hipStreamWaitEvent(pl->stream, pl->ev_twin, 0));
@@ -1872,7 +1906,20 @@ int kh_upload(kh_plan *plan, const void *emb, size_t emb_bytes, const float *mas
   if ((int64_t)emb_bytes > eb.bytes)
     fail(KH_EINVAL, "input emb has " + std::to_string(emb_bytes) + " B, the buffer " + std::to_string(eb.bytes));
   stage_common(plan, mask, mask_count, type_ids, type_count);
-  plan->emb_host.assign((const uint8_t *)emb, (const uint8_t *)emb + emb_bytes);
+  // only the rows the mask marks valid (each sequence's prefix) are ever packed: copy those, at
+  // their padded positions (a ragged batch of 256 at L = 512 holds ~10 % valid rows)
+  const size_t row = (size_t)plan->E * (plan->f16 ? 2 : 4);
+  const size_t L = plan->L, M = L * plan->B;
+  if (plan->emb_host.size() != M * row) plan->emb_host.assign(M * row, 0);
+  plan->emb_valid = emb_bytes;
+  for (int b = 0; b < plan->B; b++) {
+    const float *m = plan->mask_host.data() + (size_t)b * L;
+    size_t len = 0;
+    while (len < L && m[len] > 0.5f) len++;
+    const size_t from = (size_t)b * L * row;
+    const size_t n = from >= emb_bytes ? 0 : std::min(len * row, emb_bytes - from);
+    if (n) memcpy(plan->emb_host.data() + from, (const uint8_t *)emb + from, n);
+  }
   plan->by_ids = false;
   KH_API_END
 }
@@ -1973,6 +2020,28 @@ int kh_last_run_ms(kh_plan *plan, float *ms) {
   if (!plan->ran) fail(KH_EINVAL, "no run yet");
   KH_CHECK(hipEventSynchronize(plan->ev1));
   KH_CHECK(hipEventElapsedTime(ms, plan->ev0, plan->ev1));
+  KH_API_END
+}
+
+int kh_plan_read_buffer(kh_plan *plan, const char *id, int32_t half, void *out, size_t bytes) {
+  KH_API_BEGIN
+  if (!plan || !id || (!out && bytes)) fail(KH_EINVAL, "null argument");
+  require_live(plan->ctx);
+  kh_plan *p = plan;
+  if (half) {
+    if (!plan->twin || plan->split <= 0) fail(KH_EINVAL, "the last run did not split the batch");
+    p = plan->twin;
+  }
+  auto it = p->bufs.find(id);
+  if (it == p->bufs.end() || !it->second.mem) fail(KH_EINVAL, std::string("plan buffer ") + id + " has no device memory");
+  const size_t n = std::min(bytes, it->second.mem->bytes);
+  try {
+    KH_CHECK(hipStreamSynchronize(p->stream));
+    if (n) KH_CHECK(hipMemcpy(out, it->second.mem->p, n, hipMemcpyDeviceToHost));
+  } catch (const Error &e) {
+    latch(plan->ctx, e);
+    throw;
+  }
   KH_API_END
 }
 

@@ -3,11 +3,27 @@ for the same inputs, and the reference's parity rules (src/encoder.ts, convert/k
 from __future__ import annotations
 
 import copy
+import json
 
 import numpy as np
 
 from kleinhirn_amd import configs, inputs, synth
 from kleinhirn_amd.plan.build import build_plan
+
+
+_WEIGHTS: dict = {}
+
+
+def seeded_weights(spec: dict, head: dict) -> dict:
+    """configs.make_weights(spec, head), generated once per process (a RoBERTa-base set takes
+    seconds); each caller gets its own dict over the shared read-only arrays."""
+    key = json.dumps([spec, head], sort_keys=True)
+    if key not in _WEIGHTS:
+        w = configs.make_weights(spec, head)
+        for v in w.values():
+            v.setflags(write=False)
+        _WEIGHTS[key] = w
+    return dict(_WEIGHTS[key])
 
 
 class Case:
@@ -18,7 +34,7 @@ class Case:
         self.head = head
         self.ids = ids
         self.length = length
-        self.weights = weights if weights is not None else configs.make_weights(spec, head)
+        self.weights = weights if weights is not None else seeded_weights(spec, head)
 
     @property
     def lengths(self):

@@ -1,12 +1,12 @@
 // Runs one exported plan through kh_addon.node the way hip-backend.ts drives it (weights, check,
 // runner with init tables, upload, run, asynchronous readback) and writes the f32 output.
-//   node run_plan.js <case dir>       (files written by kleinhirn_amd.node_case.export_case)
+//   node run_plan.js <case dir>       (files written by tests/node_case.py export_case)
 'use strict';
 const fs = require('fs');
 const path = require('path');
 
 const dir = process.argv[2];
-const addon = require(process.env.KH_ADDON || path.join(__dirname, 'kh_addon.node'));
+const addon = require(process.env.KH_ADDON || path.join(__dirname, '..', '..', 'kleinhirn_amd', 'node', 'kh_addon.node'));
 const read = (f) => fs.readFileSync(path.join(dir, f));
 const meta = JSON.parse(read('meta.json'));
 const planText = read('plan.json').toString();

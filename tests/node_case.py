@@ -1,5 +1,5 @@
-"""Exports a plan, its weights and one RunInput as files for kleinhirn_amd/node/run_plan.js, so the
-Node-API path (the host side hip-backend.ts uses) runs the same case as the Python host."""
+"""Exports a plan, its weights and one RunInput as files for tests/node/run_plan.js, so the Node-API
+path (the host side hip-backend.ts uses) runs the same case as the Python host."""
 from __future__ import annotations
 
 import json
@@ -8,10 +8,10 @@ import subprocess
 
 import numpy as np
 
-from .plan.build import plan_inits, plan_json
+from kleinhirn_amd.plan.build import plan_inits, plan_json
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-ADDON = os.path.join(HERE, "node", "kh_addon.node")
+ADDON = os.path.join(os.path.dirname(HERE), "kleinhirn_amd", "node", "kh_addon.node")
 RUNNER = os.path.join(HERE, "node", "run_plan.js")
 
 

@@ -14,7 +14,7 @@ from kleinhirn_amd import backend as B
 from kleinhirn_amd import configs, inputs
 from kleinhirn_amd.plan.build import build_plan
 from oracle import manifest_format as MF
-from tests.helpers import hip_outputs
+from tests.helpers import decision_parity, hip_outputs
 from tests.test_gpu_models import case_and_oracle
 
 pytestmark = pytest.mark.gpu
@@ -37,7 +37,7 @@ def run_ids(be, case, f16=True):
 
 @pytest.mark.parametrize("version", [3, 2])
 def test_manifest_load_equals_tensor_by_tensor_upload(version):
-    case, _ = case_and_oracle("c2")
+    case, ref = case_and_oracle("c2")
     want = hip_outputs(case, f16=True)
     with tempfile.TemporaryDirectory() as d:
         path = MF.write_manifest(d, case.weights, "f16", version=version, chunk_rows=20_000)
@@ -48,7 +48,10 @@ def test_manifest_load_equals_tensor_by_tensor_upload(version):
     W = configs.storage(case.weights, True)
     assert (info["words_rows"], info["words_width"]) == W["embeddings.word.weight"].shape
     assert be.weight_bytes == sum(t.nbytes for n, t in W.items() if n != MF.WORDS)
-    assert np.array_equal(hip_outputs(case, f16=True, backend=be), want)  # host gather
+    loaded = hip_outputs(case, f16=True, backend=be)                        # host gather
+    d = decision_parity(ref, loaded)
+    assert d["mismatched"] == 0 and d["delta"] <= 2e-2, d                   # the oracle's bars
+    assert np.array_equal(loaded, want)
     assert np.array_equal(run_ids(be, case), want)                          # device table from the files
     be.dispose()
 

@@ -1,6 +1,7 @@
-"""The batch scheduler (kh_sched_run) against one batch plan per case: each sequence's result does
-not depend on its batch-mates, plan length or chunk (the batch/single identity of
-test_gpu_models), so the scheduled outputs equal the batch plan's bit for bit."""
+"""The batch scheduler (kh_sched_run) against the oracle's golden outputs of each case, and against
+one batch plan per case: each sequence's result does not depend on its batch-mates, plan length or
+chunk (the batch/single identity of test_gpu_models), so the scheduled outputs equal the batch
+plan's bit for bit."""
 from __future__ import annotations
 
 import numpy as np
@@ -9,7 +10,7 @@ import pytest
 from kleinhirn_amd import configs
 from kleinhirn_amd.backend import HipBackend, KhError
 from kleinhirn_amd.scheduler import BatchScheduler
-from tests.helpers import hip_outputs
+from tests.helpers import decision_parity, hip_outputs
 from tests.test_gpu_models import case_and_oracle
 
 pytestmark = pytest.mark.gpu
@@ -17,7 +18,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("key", ["c2", "c5"])
 def test_scheduled_outputs_equal_the_batch_plan(key):
-    case, _ = case_and_oracle(key)
+    case, ref = case_and_oracle(key)
     want = hip_outputs(case, f16=True)
     W = configs.storage(case.weights, True)
     be = HipBackend(W)
@@ -26,6 +27,8 @@ def test_scheduled_outputs_equal_the_batch_plan(key):
     n = [len(x) for x in case.ids]
     out, st = sch.run(case.ids)
     print(key, st)
+    d = decision_parity(ref, out)
+    assert d["mismatched"] == 0 and d["delta"] <= 2e-2, d
     assert np.array_equal(out, want)
     assert st["sequences"] == len(n) and st["tokens"] == sum(n) and st["chunks"] >= -(-len(n) // 4)
     budget = max(n) + 10

@@ -1,5 +1,5 @@
 """The Node-API path hip-backend.ts uses (kh_addon.node over libkh_hip.so), driven by
-kleinhirn_amd/node/run_plan.js: structural plan checks on the CPU, and on the GPU the same case as
+tests/node/run_plan.js: structural plan checks on the CPU, and on the GPU the same case as
 the Python host, compared bit for bit and against the golden oracle vectors."""
 from __future__ import annotations
 
@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from kleinhirn_amd import configs, inputs
-from kleinhirn_amd.node_case import ADDON, export_case, run_node
+from tests.node_case import ADDON, export_case, run_node
 from kleinhirn_amd.plan.build import build_plan
 
 pytestmark = pytest.mark.skipif(shutil.which("node") is None or not os.path.exists(ADDON),
@@ -122,7 +122,7 @@ def test_node_manifest_load_and_device_gather_match_python_path():
     from oracle import manifest_format as MF
     from tests.helpers import hip_outputs
     from tests.test_gpu_models import case_and_oracle
-    case, _ = case_and_oracle("c2")
+    case, ref = case_and_oracle("c2")
     plan = build_plan(case.spec, case.head, case.length, len(case.ids), True)
     mask, tt = inputs.mask_and_types(case.spec, case.ids, case.length)
     ids = np.zeros(case.length * len(case.ids), dtype=np.int32)
@@ -135,6 +135,9 @@ def test_node_manifest_load_and_device_gather_match_python_path():
         res = run_node(d)
         got = np.fromfile(os.path.join(d, "out.bin"), dtype=np.float32).reshape(len(case.ids), -1)
     assert res["ok"] and res["manifest"]["tensors"] > 0
+    from tests.helpers import decision_parity
+    d = decision_parity(ref, got)
+    assert d["mismatched"] == 0 and d["delta"] <= 2e-2, d  # the oracle's bars
     assert np.array_equal(got, hip_outputs(case, f16=True))
 
 
@@ -162,11 +165,11 @@ def test_node_addon_scores_and_rank_equal_the_oracle():
 def test_node_scheduler_matches_python_path():
     """schedCreate / schedRun through the addon: two copies of a batch-4 plan run the c2 case in
     length-ordered chunks; outputs equal the Python host's batch plan bit for bit."""
-    from kleinhirn_amd.node_case import export_sched_case
+    from tests.node_case import export_sched_case
     from kleinhirn_amd.scheduler import type_words
     from tests.helpers import hip_outputs
     from tests.test_gpu_models import case_and_oracle
-    case, _ = case_and_oracle("c2")
+    case, ref = case_and_oracle("c2")
     W = configs.storage(case.weights, True)
     words = W.pop("embeddings.word.weight")
     plan = build_plan(case.spec, case.head, case.length, 4, True)
@@ -175,4 +178,7 @@ def test_node_scheduler_matches_python_path():
         res = run_node(d)
         got = np.fromfile(os.path.join(d, "out.bin"), dtype=np.float32).reshape(len(case.ids), -1)
     assert res["ok"] and res["stats"]["sequences"] == len(case.ids)
+    from tests.helpers import decision_parity
+    d = decision_parity(ref, got)
+    assert d["mismatched"] == 0 and d["delta"] <= 2e-2, d  # the oracle's bars
     assert np.array_equal(got, hip_outputs(case, f16=True))
