@@ -131,6 +131,14 @@ def build_plan(spec: dict, head: dict, length: int, batch: int, f16: bool, marke
                 "bind": bind, "dispatch": [math.ceil(n / 16), ydim]}
 
     segments = []
+    # capture slots (the capture tool copies these buffers after their segment, an f32 row block
+    # each; src/plan/build.ts:142-144)
+    slot = [0]
+
+    def take(*bufs):
+        out = [{"buffer": b, "slot": slot[0] + i} for i, b in enumerate(bufs)]
+        slot[0] += len(bufs)
+        return out
     emb = spec["embed"]
     emb_w = f"w:{names.embedNormW}"
     emb_b = f"w:{names.embedNormB}" if names.embedNormB else "zero"
@@ -139,7 +147,7 @@ def build_plan(spec: dict, head: dict, length: int, batch: int, f16: bool, marke
         type_table = "w:embeddings.type.weight" if emb["typeVocab"] > 0 else "zero"
         if emb["project"]:
             raise ValueError("embedding projection (ELECTRA) is not described here")
-        segments.append({"name": "embed", "prefix": "", "ops": [{
+        segments.append({"name": "embed", "prefix": "", "capture": take("x"), "ops": [{
             "name": "embed", "kernel": "embln",
             "constants": {"N": E, "L": length, "OFFSET": emb["positionOffset"] if absolute else 0,
                           "MAXPOS": emb["maxPositions"] if absolute else 1, "EPS": emb["norm"]["eps"],
@@ -148,10 +156,16 @@ def build_plan(spec: dict, head: dict, length: int, batch: int, f16: bool, marke
             "bind": ["emb", "w:embeddings.position.weight" if absolute else "zero", type_table,
                      "typeIds", emb_w, emb_b, "mask", "x"],
             "dispatch": ["rows", 1]}]})
-    else:
-        mode = 1 if emb["maskMultiply"] else 0
+    elif emb["maskMultiply"]:
+        # the capture tool records the plain norm too (captureOps run only when capturing)
         segments.append({"name": "embed", "prefix": "",
-                         "ops": [ln("embed", mode, ["emb", "dummy", emb_w, emb_b, "mask", "x"])]})
+                         "ops": [ln("embed", 1, ["emb", "dummy", emb_w, emb_b, "mask", "x"])],
+                         "captureOps": [ln("embedPlain", 0, ["emb", "dummy", emb_w, emb_b, "mask", "tmp"])],
+                         "capture": take("tmp", "x")})
+    else:
+        segments.append({"name": "embed", "prefix": "",
+                         "ops": [ln("embed", 0, ["emb", "dummy", emb_w, emb_b, "mask", "x"])],
+                         "capture": take("x")})
 
     rel = spec["attention"].get("rel") if spec["attention"]["kind"] == "deberta-relative" else None
     if rel is not None:
@@ -183,18 +197,19 @@ def build_plan(spec: dict, head: dict, length: int, batch: int, f16: bool, marke
             tt = dict(t, attnNormW=None) if identity else t
             table = ("cossinG" if a_window == 0 else "cossinL") if rope_split else "cossin"
             ops = pre_norm_layer(dims, tt, "x", not identity, a_scale, a_window, bool(rope), ffn, table)
-        segments.append({"name": f"layer{l}", "prefix": f"L{l}.", "ops": ops, "skippable": True})
+        segments.append({"name": f"layer{l}", "prefix": f"L{l}.", "ops": ops, "skippable": True,
+                         "capture": take("x")})
 
     stream = "x"
     if spec["block"]["finalNorm"]:
-        segments.append({"name": "final", "prefix": "", "ops": [
+        segments.append({"name": "final", "prefix": "", "capture": take("tmp"), "ops": [
             ln("final", 0, ["x", "dummy", f"w:{names.finalNormW}",
                             f"w:{names.finalNormB}" if names.finalNormB else "zero", "mask", "tmp"])]})
         stream = "tmp"
 
     if not pooled:
         return _marker_plan(spec, head, segments, stream, dims, length, batch, f16, markers, K, bytes_of, mm, ln,
-                            absolute)
+                            absolute, take, slot)
 
     # Head (src/plan/build.ts:296-357)
     head_buffers = []
@@ -316,12 +331,12 @@ def build_plan(spec: dict, head: dict, length: int, batch: int, f16: bool, marke
         "buffers": decls, "segments": segments, "inputs": inputs,
         "output": {"buffer": prev, "bytes": bytes_of(out_rows * width), "dtype": "storage",
                    "rows": out_rows, "cols": width},
-        "captureSlots": 0, "captureSlotBytes": length * H * 4,
+        "captureSlots": slot[0], "captureSlotBytes": length * H * 4,
     }
 
 
 def _marker_plan(spec, head, segments, stream, dims, length, batch, f16, markers, K, bytes_of, mm, ln,
-                 absolute) -> dict:
+                 absolute, take, slot) -> dict:
     """Marker heads, whose output is one f32 logit per marker slot (K = markers x batch slots; the
     packed markers input holds per sequence K row indices, K mask words as f32 bits, K group ids):
     * gliner2 (src/plan/build.ts:358-377): the hidden states at the marker rows, fc1 with ReLU,
@@ -349,12 +364,12 @@ def _marker_plan(spec, head, segments, stream, dims, length, batch, f16, markers
     else:
         if stream != "tmp":
             raise ValueError("julia head expects a final norm")
-        segments.append({"name": "typed", "prefix": "", "ops": [
+        segments.append({"name": "typed", "prefix": "", "capture": take("tmp"), "ops": [
             {"name": "type", "kernel": "add", "constants": {"TOTAL": M * H, "N": H, "MODE": 1, "L": length},
              "bind": ["tmp", "typeRow"], "dispatch": [add_workgroups(M, H), 1]}]})
         row_select = {"table": "w:type_emb.weight", "dst": "typeRow", "rowBytes": bytes_of(H)}
         for i in range(int(head["layers"])):
-            segments.append({"name": f"head{i}", "prefix": f"head{i}.", "ops": pre_norm_layer(
+            segments.append({"name": f"head{i}", "prefix": f"head{i}.", "capture": take("tmp"), "ops": pre_norm_layer(
                 dims, julia_head_layer(i), "tmp", True, (H / spec["heads"]) ** -0.5, 0, False,
                 {"kind": "mlp", "width": int(head["ffn"]), "act": 1})})
         segments.append({"name": "scorer", "prefix": "scorer.", "ops": [
@@ -433,7 +448,7 @@ def _marker_plan(spec, head, segments, stream, dims, length, batch, f16, markers
         "buffers": decls, "segments": segments,
         "inputs": {"embeddings": "emb", "mask": "mask", "markers": "packed"},
         "output": {"buffer": "logits", "bytes": K * 4, "dtype": "f32", "rows": K, "cols": 1},
-        "captureSlots": 0, "captureSlotBytes": length * H * 4,
+        "captureSlots": slot[0], "captureSlotBytes": length * H * 4,
     }
     if row_select:
         plan["rowSelect"] = row_select

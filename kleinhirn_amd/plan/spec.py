@@ -138,6 +138,20 @@ def deberta_v3(hidden: int, layers: int, heads: int, intermediate: int, vocab: i
     }
 
 
+def gliner(enc: dict, temperature: float, head_hidden: int | None = None, markers: int = 16) -> tuple[dict, dict]:
+    """specFromGlinerManifest (src/plan/spec.ts:214-246): the DeBERTa-v2 encoder of a GLiNER2
+    manifest (relative c2p+p2c attention, embedding LayerNorm times the mask, no position or type
+    table) and the gliner2 span head. `enc` holds the manifest's encoder fields (hiddenSize,
+    layers, heads, intermediateSize, positionBuckets, maxRelativePositions, layerNormEps,
+    vocabSize)."""
+    spec = deberta_v3(enc["hiddenSize"], enc["layers"], enc["heads"], enc["intermediateSize"],
+                      enc.get("vocabSize", 0), enc["positionBuckets"], enc["maxRelativePositions"],
+                      enc["layerNormEps"])
+    spec["embed"]["maxPositions"] = 0
+    head = {"type": "gliner2", "hidden": int(head_hidden or 768), "temperature": temperature, "markers": markers}
+    return spec, head
+
+
 def deberta_classify_head(hidden: int, classes: int, pooler_act: str = "gelu") -> dict:
     """ContextPooler (first token, dense, pooler_hidden_act) then the classifier
     (src/plan/hf.ts:354-364)."""

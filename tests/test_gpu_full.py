@@ -93,3 +93,40 @@ def test_scheduler_full_batch_matches_oracle(name):
     assert d["delta"] <= 2e-2, d
     if ref.shape[1] > 1:
         assert d["mismatched"] == 0, d
+
+
+def test_split_full_batch_is_deterministic(monkeypatch):
+    """The whole c2 batch on two streams, run repeatedly, equals the one-stream run bit for bit.
+    (Regression: a GEMM slab barrier that did not wait for the wavefront's own LDS reads let a
+    delayed read return the next slab's data when another stream's kernels shared the CU, and 10-40
+    of the 256 f16 outputs changed from run to run.)"""
+    from kleinhirn_amd import configs, inputs
+    from kleinhirn_amd.backend import HipBackend
+    from kleinhirn_amd.plan.build import build_plan
+    case, ref = full_case("c2_full")
+    W = configs.storage(case.weights, True)
+    be = HipBackend(W)
+    B, L = len(case.ids), case.length
+    ri = inputs.run_input(case.spec, W["embeddings.word.weight"], case.ids, L)
+
+    def runs(n):
+        r = be.runner(build_plan(case.spec, case.head, L, B, True))
+        r.upload(ri)
+        outs = []
+        for _ in range(n):
+            r.run(L * B)
+            outs.append(r.read_output().reshape(B, -1))
+        streams = r.info.streams
+        r.destroy()
+        return outs, streams
+
+    monkeypatch.setenv("KH_NO_SPLIT", "1")
+    (whole,), s1 = runs(1)
+    monkeypatch.delenv("KH_NO_SPLIT")
+    split, s2 = runs(6)
+    be.dispose()
+    assert (s1, s2) == (1, 2)
+    for i, o in enumerate(split):
+        assert np.array_equal(o, whole), (i, int((np.abs(o - whole).max(1) > 0).sum()))
+    d = decision_parity(ref, whole)
+    assert d["mismatched"] == 0, d

@@ -279,6 +279,57 @@ def test_relative_attention(f16, lens, split):
     close(out[valid], want[valid], 1e-2 if f16 else 1e-5, f"relative attention {lens}")
 
 
+def rel_attention_ref_rows(qkv, lens, L, H, D, scale, idx, pk, pq, chunk=64):
+    """The relative attention of attention_ref, a block of query rows at a time (a 1280-row
+    sequence's [n, n, D] position gathers would not fit in memory at once)."""
+    hd = H * D
+    out = np.zeros((L * len(lens), hd))
+    q64 = qkv.astype(np.float64)
+    for b, n in enumerate(lens):
+        rows = q64[b * L:b * L + n]
+        j = np.arange(n)
+        for h in range(H):
+            k = rows[:, (H + h) * D:(H + h + 1) * D]
+            v = rows[:, (2 * H + h) * D:(2 * H + h + 1) * D]
+            pkh, pqh = pk[:, h * D:(h + 1) * D], pq[:, h * D:(h + 1) * D]
+            for i0 in range(0, n, chunk):
+                i = np.arange(i0, min(n, i0 + chunk))
+                q = rows[i, h * D:(h + 1) * D]
+                p = idx[i[:, None] * L + j[None, :]]
+                s = q @ k.T + (q @ pkh.T)[np.arange(len(i))[:, None], p] + (k @ pqh.T)[j[None, :], p]
+                s = s / scale
+                s = s - s.max(1, keepdims=True)
+                e = np.exp(s)
+                out[b * L + i, h * D:(h + 1) * D] = (e / e.sum(1, keepdims=True)) @ v
+    return out
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_relative_attention_long_plan(f16):
+    """GLiNER-base length (L = 1280, the reference's tests/helpers/plan-trace.ts:50) with its
+    bucket table (256 log buckets, max distance 512): one full sequence and one of 700 rows, the
+    fused DeBERTa attention against float64."""
+    H, D = 2, 64
+    L, lens = 1280, [1280, 700]
+    B = len(lens)
+    hd = H * D
+    span, maxpos = 256, 512
+    dt = np.float16 if f16 else np.float32
+    qkv = (RNG.standard_normal((L * B, 3 * hd)) * 0.5).astype(dt)
+    pk = (RNG.standard_normal((2 * span, hd)) * 0.5).astype(dt)
+    pq = (RNG.standard_normal((2 * span, hd)) * 0.5).astype(dt)
+    idx = rel_pos_table(L, span, maxpos)
+    mask = prefix_mask(L, lens)
+    scale = math.sqrt(3 * D)
+    ops = [{"name": "a", "kernel": "attention", "constants": {"L": L, "H": H, "D": D, "SCALE": scale},
+            "bind": ["emb", "w:pk", "w:pq", "relidx", "mask", "ctx"], "dispatch": [H, "rows"]}]
+    plan = mini_plan(f16, L, B, 3 * hd, ops, {"relidx": idx, "ctx": L * B * hd}, "ctx", hd)
+    out = run_plan(plan, {"pk": pk, "pq": pq}, qkv, mask, L * B).reshape(L * B, hd)
+    want = rel_attention_ref_rows(qkv, lens, L, H, D, scale, idx, pk.astype(np.float64), pq.astype(np.float64))
+    valid = mask > 0.5
+    close(out[valid], want[valid], 1e-2 if f16 else 1e-5, f"relative attention L {L}")
+
+
 @pytest.mark.parametrize("f16", [False, True])
 def test_add_geglu_rope_pool_gather(f16):
     L, lens = 7, [3, 7]
