@@ -32,10 +32,13 @@ PEAK = {"f16_mfma_tflops": 2500.0, "f32_mfma_tflops": 157.3, "hbm_gbs": 8000.0}
 # bench (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch averaged over the family), each counter scaled
 # by what it reads for a plain device copy of 1 GiB (python3 -m kleinhirn_amd.profiling copy 1024:
 # FETCH_SIZE reads 0.5 GiB -> x2.0, WRITE_SIZE reads 1.0 GiB -> x1.0). Summaries with the commands:
-# profiles/gemm_mfma_c2_roberta_base_ragged256_traffic.md. Re-measured whenever the kernel changes.
+# profiles/gemm_mfma_c2_roberta_base_ragged256_traffic.md and layernorm_c5_xlmr_minilm_l12_pairs4096_traffic.md.
+# Re-measured whenever the kernel changes (an entry whose source digest differs is not reported).
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
 TRAFFIC_KIB = {  # (workload, family): (FETCH_SIZE KiB, WRITE_SIZE KiB) per dispatch, kernel source sha256[:16]
-    ("c2-roberta-base-f16-ragged256", "gemm_mfma"): (54097.1, 40025.3, "9bbde0fd85b000a9"),
+    ("c2-roberta-base-f16-ragged256", "gemm_mfma"): (54870.8, 40025.3, "8e74ae882aff4f66"),
+    ("c5-xlmr-minilm-l12-f16-pairs4096", "gemm_mfma"): (816807.1, 1894393.1, "8e74ae882aff4f66"),
+    ("c5-xlmr-minilm-l12-f16-pairs4096", "layernorm"): (834311.3, 834276.7, "453e153b2ec07c8c"),
 }
 # the source file of each kernel family (a counter figure measured on other code is not reported)
 FAMILY_SOURCE = {"gemm_mfma": "gemm.hip", "attention": "attention.hip", "layernorm": "rowops.hip",

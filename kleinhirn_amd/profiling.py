@@ -3,7 +3,7 @@ per-launch profile (kh_profile) reports, so a kernel trace can be checked agains
 HIP-event timings and PMC byte counters can be set against a launch's algorithmic bytes.
 
     python3 -m kleinhirn_amd.profiling copy <MiB>            plain device copy (counter calibration)
-    python3 -m kleinhirn_amd.profiling trace <rocprof dir>   kernel-trace summary (markdown)
+    python3 -m kleinhirn_amd.profiling trace <rocprof dir>   kernel-trace summary by family and by kernel (markdown)
     python3 -m kleinhirn_amd.profiling pmc <rocprof dir> ... counter sums per family (markdown)
 
 The copy mode is the calibration workload: FETCH_SIZE and WRITE_SIZE of one copy of N bytes should
@@ -15,6 +15,7 @@ import collections
 import csv
 import glob
 import os
+import re
 import sqlite3
 import sys
 
@@ -89,6 +90,32 @@ def trace_summary(d: str) -> str:
     return "\n".join(lines)
 
 
+def short_name(name: str) -> str:
+    """Demangled-looking kernel name without namespaces and argument lists."""
+    n = re.sub(r"kh::(\(anonymous namespace\)::)?", "", name)
+    n = re.sub(r"\([^()]*\)$", "", n.strip())
+    return n.replace("void ", "").strip()[:90]
+
+
+def kernel_table(d: str, top: int = 16) -> str:
+    """The `top` kernels (template instance and grid) by total time of a --kernel-trace run."""
+    per = collections.defaultdict(list)
+    for name, grid, ns in kernel_grids(d):
+        per[(short_name(name), grid)].append(ns)
+    total = sum(sum(v) for v in per.values())
+    lines = ["| kernel | grid (work-items) | launches | avg us | total ms | % |", "|---|---|---|---|---|---|"]
+    for (name, grid), v in sorted(per.items(), key=lambda kv: -sum(kv[1]))[:top]:
+        lines.append(f"| {name} | {grid} | {len(v)} | {sum(v) / len(v) / 1e3:.2f} | {sum(v) / 1e6:.3f} | "
+                     f"{100 * sum(v) / total:.1f} |")
+    return "\n".join(lines)
+
+
+def kernel_grids(d: str) -> list[tuple[str, str, float]]:
+    return [(r["Kernel_Name"], "x".join(r.get(f"Grid_Size_{a}", "?") for a in "XYZ").replace("x1x1", ""),
+             float(r["End_Timestamp"]) - float(r["Start_Timestamp"]))
+            for r in _csv_rows(d, "kernel_trace.csv")]
+
+
 def pmc_sums(d: str) -> dict[str, dict[str, float]]:
     """family -> {counter: summed value, 'dispatches': n} from a --pmc run (csv output)."""
     acc: dict = collections.defaultdict(lambda: collections.defaultdict(float))
@@ -134,6 +161,8 @@ def main(argv: list[str]) -> int:
         copy_probe(int(argv[1]))
     elif len(argv) >= 2 and argv[0] == "trace":
         print(trace_summary(argv[1]))
+        print()
+        print(kernel_table(argv[1]))
     elif len(argv) >= 2 and argv[0] == "pmc":
         print(pmc_summary(argv[1:]))
     else:
