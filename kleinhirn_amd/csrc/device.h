@@ -48,14 +48,23 @@ __device__ __forceinline__ int xcd_tile(int tile, int nblk) {
 }
 
 // GELU by erf through Abramowitz-Stegun 7.1.26 (the reference's constants, src/wasm/plan.ts:99-107)
+// erf(x) = 1 - P(t) exp(-x^2), t = 1 / (1 + p x) for x = |v| / sqrt 2 >= 0, so with
+// R = P exp(-v^2 / 2) / 2: gelu(v) = v - v R for v >= 0 and v R below. The 1/2 is folded into the
+// polynomial's coefficients (exact: a power of two), 1/sqrt 2 into p and the exponent goes to the
+// hardware exp2; 12 VALU operations and two transcendentals per value, within 5e-7 of the
+// reference's arrangement of the same formula.
 __device__ __forceinline__ float gelu_as(float v) {
-  float u = v * 0.7071067811865476f;
   // hardware reciprocal (1 ulp): the formula's own error is 1.5e-7 absolute
-  float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * fabsf(u));
-  float p = (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
-             0.254829592f) * t;
-  float e = 1.0f - p * __expf(-u * u);
-  return 0.5f * v * (1.0f + (v >= 0.0f ? e : -e));
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f * 0.7071067811865476f, fabsf(v), 1.0f));
+  float p = __builtin_fmaf(0.5f * 1.061405429f, t, 0.5f * -1.453152027f);
+  p = __builtin_fmaf(p, t, 0.5f * 1.421413741f);
+  p = __builtin_fmaf(p, t, 0.5f * -0.284496736f);
+  p = __builtin_fmaf(p, t, 0.5f * 0.254829592f);
+  p = p * t;
+  const float e = __builtin_amdgcn_exp2f((v * v) * (-0.5f * 1.4426950408889634f));
+  // w carries the sign of v: max(v, 0) - |w| is v - w for v >= 0 and w below
+  const float w = v * (p * e);
+  return fmaxf(v, 0.0f) - fabsf(w);
 }
 
 __device__ __forceinline__ float activate(float v, int act) {

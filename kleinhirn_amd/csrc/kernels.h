@@ -92,9 +92,10 @@ void embln(bool f16, const EmbLnArgs &a, const Packing &p, hipStream_t s);
 void mask_logits(bool f16, const void *raw, const uint32_t *packed, float *logits, int K, float temp, int64_t total,
                  hipStream_t s);
 
-// LN over rows: MODE 2 adds b first. rows = T (packed) or B (sequence rows).
+// LN over rows: MODE 2 adds b first. rows = T (packed) or B (sequence rows). With ids, row r is
+// row ids[r] of a (the device word table), with the arithmetic of the same LN over gathered rows.
 void layernorm(bool f16, const void *a, const void *b, const void *gamma, const void *beta, void *out,
-               int64_t rows, int N, float eps, hipStream_t s);
+               int64_t rows, int N, float eps, hipStream_t s, const int32_t *ids = nullptr);
 
 // dst += src (MODE 0) or dst[r] += src[seq(r)] (MODE 1), rounded to storage.
 void add(bool f16, void *dst, const void *src, int64_t rows, int N, int mode, const Packing &p,

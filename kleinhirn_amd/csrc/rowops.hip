@@ -54,11 +54,12 @@ __device__ __forceinline__ void ln_finish(float (&v)[PER][VEC], int N, const T *
 template <typename T, int VEC, int PER>
 __global__ void __launch_bounds__(256) layernorm_kernel(const T *__restrict__ a, const T *__restrict__ b,
                                                         const T *__restrict__ gamma, const T *__restrict__ beta,
-                                                        T *__restrict__ out, int64_t rows, int N, float eps) {
+                                                        T *__restrict__ out, int64_t rows, int N, float eps,
+                                                        const int32_t *__restrict__ ids) {
   int lane = threadIdx.x & 63;
   int64_t r = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
   if (r >= rows) return;
-  const T *ar = a + r * N;
+  const T *ar = a + (ids ? (int64_t)ids[r] : r) * N;
   const T *br = b ? b + r * N : nullptr;
   float v[PER][VEC];
 #pragma unroll
@@ -88,17 +89,19 @@ template <typename T, int LPR, int PER>
 __global__ void __launch_bounds__(256) layernorm_rows_kernel(const T *__restrict__ a, const T *__restrict__ b,
                                                              const T *__restrict__ gamma,
                                                              const T *__restrict__ beta, T *__restrict__ out,
-                                                             int64_t rows, int N, float eps) {
+                                                             int64_t rows, int N, float eps,
+                                                             const int32_t *__restrict__ ids) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int RPW = WAVE / LPR;  // rows per wavefront
   const int lane = threadIdx.x & 63, l = lane % LPR;
   const int64_t r = ((int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6)) * RPW + lane / LPR;
   if (r >= rows) return;  // whole groups leave together: the shuffles below stay in a group
+  const T *ar = a + (ids ? (int64_t)ids[r] : r) * N;
   float v[PER][VEC];
 #pragma unroll
   for (int k = 0; k < PER; k++) {
     const int e0 = (k * LPR + l) * VEC;
-    VecIO<T, VEC>::load(a + r * N + e0, v[k]);
+    VecIO<T, VEC>::load(ar + e0, v[k]);
     if (b) {
       float y[VEC];
       VecIO<T, VEC>::load(b + r * N + e0, y);
@@ -199,7 +202,7 @@ bool dispatch_per(int N, F &&f) {
 
 template <typename T>
 void layernorm_t(const void *a, const void *b, const void *gamma, const void *beta, void *out, int64_t rows,
-                 int N, float eps, hipStream_t s) {
+                 int N, float eps, const int32_t *ids, hipStream_t s) {
   // rows of 3 x 2^j 16-byte chunks (384- and 768-wide f16, 384-wide f32): groups of 2^j lanes
   constexpr int VEC16 = 16 / sizeof(T);
   if (N % (3 * VEC16) == 0) {
@@ -208,7 +211,7 @@ void layernorm_t(const void *a, const void *b, const void *gamma, const void *be
       constexpr int LPR = decltype(lpr_t)::value;
       const int64_t per_block = (int64_t)ROWS_PER_BLOCK * (WAVE / LPR);
       launch((layernorm_rows_kernel<T, LPR, 3>), dim3((unsigned)((rows + per_block - 1) / per_block)), dim3(256),
-             0, s, (const T *)a, (const T *)b, (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps);
+             0, s, (const T *)a, (const T *)b, (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps, ids);
     };
     switch (lpr) {
       case 8: go_rows(std::integral_constant<int, 8>()); return;
@@ -224,7 +227,7 @@ void layernorm_t(const void *a, const void *b, const void *gamma, const void *be
     dispatch_per<T, VEC>(N, [&](auto per) {
       constexpr int PER = decltype(per)::value;
       launch((layernorm_kernel<T, VEC, PER>), grid, dim3(256), 0, s, (const T *)a, (const T *)b,
-                         (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps);
+                         (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps, ids);
     });
   };
   // 16-byte loads where the width allows
@@ -410,10 +413,10 @@ void first_rows(bool f16, const void *src, void *dst, int D, bool from_packed, c
 }
 
 void layernorm(bool f16, const void *a, const void *b, const void *gamma, const void *beta, void *out,
-               int64_t rows, int N, float eps, hipStream_t s) {
+               int64_t rows, int N, float eps, hipStream_t s, const int32_t *ids) {
   if (rows <= 0) return;
-  if (f16) layernorm_t<half_t>(a, b, gamma, beta, out, rows, N, eps, s);
-  else layernorm_t<float>(a, b, gamma, beta, out, rows, N, eps, s);
+  if (f16) layernorm_t<half_t>(a, b, gamma, beta, out, rows, N, eps, ids, s);
+  else layernorm_t<float>(a, b, gamma, beta, out, rows, N, eps, ids, s);
 }
 
 void embln(bool f16, const EmbLnArgs &a, const Packing &p, hipStream_t s) {

@@ -819,18 +819,11 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
     case S_LN: {
       if (pl->by_ids && s.in[0].id == pl->in_emb) {
         // the embedding LN of plans without position or type tables (DeBERTa, ModernBERT) over
-        // rows gathered from the device word table: the embln kernel with no added tables
-        EmbLnArgs a;
-        a.table = pl->ctx->words->p;
-        a.ids = (const int32_t *)pl->d_ids.p;
-        a.gamma = bufp(pl, s.in[2]);
-        a.beta = bufp(pl, s.in[3]);
-        a.out = bufp(pl, s.in[5]);
-        a.N = s.N;
-        a.posids = 1;  // no position rows: the (absent) type words are not read
-        a.eps = s.eps;
-        begin("embln", 8.0 * pl->T * s.N, 2.0 * es * pl->T * s.N + 4.0 * pl->T);
-        embln(f16, a, pk, st);
+        // rows gathered from the device word table: the same LN kernel reading row ids[r] of the
+        // table, so the result equals the LN of the uploaded rows bit for bit
+        begin("layernorm", 8.0 * pl->T * s.N, 2.0 * es * pl->T * s.N + 4.0 * pl->T);
+        layernorm(f16, pl->ctx->words->p, nullptr, bufp(pl, s.in[2]), bufp(pl, s.in[3]), bufp(pl, s.in[5]), pl->T,
+                  s.N, s.eps, st, (const int32_t *)pl->d_ids.p);
         end();
         break;
       }
