@@ -15,11 +15,13 @@
 //
 // DeBERTa relative attention adds q_i . pos_key[m] + k_j . pos_query[m] with m = bucket(i - j) to
 // q_i . k_j before the scale (src/wasm/plan.ts:791-840). The 32 queries of a wavefront and a
-// 32-key sub-tile span 63 distances i - j: per sub-tile the wavefront computes both terms for the
-// position rows of those distances (row r: bucket(dlo + r)) on MFMA (pos_key rows x its Q,
-// pos_query rows x the sub-tile's K), parks them in its own LDS scratch (row pitch 68 floats) and
-// adds each score's two entries from there, at offsets fixed by the score's register. The
-// position tables are read from L2; no [T, H, buckets] array exists.
+// 32-key sub-tile span 63 distances i - j: per sub-tile the wavefront computes each term for the
+// position rows of those distances (row r: bucket(dlo + r)) on MFMA (pos_key rows x its Q, then
+// pos_query rows x the sub-tile's K), parks it in its own LDS scratch (row pitch 68 floats) and
+// adds each score's entry from there, at offsets fixed by the score's register; the two terms
+// take turns in one scratch. The position tables are read from L2; no [T, H, buckets] array
+// exists. The bucket table (i - j -> position row) sits in LDS as 16-bit entries, sized by the
+// plan's length.
 #include <type_traits>
 
 #include "kernels.h"
@@ -30,7 +32,6 @@ namespace kh {
 namespace {
 
 constexpr int QT = ATTN_QTILE;  // queries per block (2 wavefronts x 32)
-constexpr int REL_BUCKETS = 2 * ATTN_REL_LMAX - 1;  // bucket table entries cached in LDS
 constexpr int KT = 64;          // keys per LDS tile
 
 template <typename T>
@@ -53,10 +54,10 @@ struct AttnMfma<float> {
   }
 };
 
-// Four wavefronts per SIMD on the standard path: short sequences are latency-bound. WIN: a sliding
-// window (a.window > 0) bounds the keys of each query.
+// Four wavefronts per SIMD on the standard path (short sequences are latency-bound), two on the
+// relative path. WIN: a sliding window (a.window > 0) bounds the keys of each query.
 template <typename T, int D, bool REL, bool WIN>
-__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(REL ? 1 : 4, 8)))
+__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(REL ? 2 : 4, 8)))
 attn_kernel(AttnArgs a, Packing p) {
   typedef AttnMfma<T> MF;
   constexpr int PADK = 16 / sizeof(T);   // 16 bytes of row padding
@@ -72,8 +73,8 @@ attn_kernel(AttnArgs a, Packing p) {
   __shared__ __attribute__((aligned(16))) T sK[KT * LDK];
   __shared__ __attribute__((aligned(16))) T sVt[D * LDV];
   constexpr int RP = 68;  // relative scratch pitch (floats)
-  __shared__ __attribute__((aligned(16))) float sRel[REL ? 2 * 2 * 32 * RP : 1];  // [wave][c2p|p2c][32][RP]
-  __shared__ int sBucket[REL ? REL_BUCKETS : 1];
+  __shared__ __attribute__((aligned(16))) float sRel[REL ? 2 * 32 * RP : 1];  // [wave][32][RP]
+  extern __shared__ short sBucket[];  // [2 lmax - 1] (dynamic: the relative path only)
 
   // items (head, query tile), tiles fastest: the query tiles of one sequence and head run
   // together on one XCD and find its K and V rows in that XCD's L2
@@ -116,9 +117,35 @@ attn_kernel(AttnArgs a, Packing p) {
 #pragma unroll
     for (int r = 0; r < 16; r++) o[dt][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
+  // c2p rows of one 32-row distance block for this wavefront's queries: q . pos_key[bucket(d)]
+  // for d = d0 + lane-row, as [row][query] accumulators (lane = query)
+  [[maybe_unused]] const int64_t hd = (int64_t)H * D;
+  // (the bucket table from LDS, or from global memory before the LDS copy is visible)
+  [[maybe_unused]] auto c2p_block = [&](int d0, auto from_lds_t) {
+    int di = d0 + (lane & 31) + a.lmax - 1;  // this lane's distance row
+    di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
+    // < nb: the relidx table is checked against the tables
+    const int pr = decltype(from_lds_t)::value ? (int)sBucket[di] : a.bucket[di];
+    const T *pt = (const T *)a.pos_key + pr * hd + h * D + g * MF::KLANE;
+    float16v c = {};
+#pragma unroll
+    for (int s = 0; s < QS; s++) {
+      typename MF::frag fp;
+      if constexpr (sizeof(T) == 2) fp = *reinterpret_cast<const half8v *>(pt + s * MF::KSTEP);
+      else fp = pt[s * MF::KSTEP];
+      c = MF::mma(fp, qf[s], c);
+    }
+    return c;
+  };
+  // The distance window of the sub-tile of keys kj0 .. kj0 + 31 starts at dlo = qw0 - kj0 - 31; the
+  // next sub-tile's (32 keys on) starts 32 lower, so the first half of a window's c2p rows is the
+  // second half of the next one's: each sub-tile computes one block and carries it to the next.
+  // The carry into the first sub-tile is computed here.
+  [[maybe_unused]] float16v c2p_carry;
   if constexpr (REL) {
     // visible to every wavefront after the first K/V staging barrier
-    for (int i = t; i < 2 * a.lmax - 1; i += 128) sBucket[i] = a.bucket[i];
+    for (int i = t; i < 2 * a.lmax - 1; i += 128) sBucket[i] = (short)a.bucket[i];
+    c2p_carry = c2p_block(q0 + w * 32 - (klo + 31) + 32, std::false_type{});
   }
 
   for (int kb = klo; kb < khi; kb += KT) {
@@ -177,56 +204,65 @@ attn_kernel(AttnArgs a, Packing p) {
     float tmax = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
-      [[maybe_unused]] const float *c2pW = nullptr;
-      [[maybe_unused]] const float *p2cW = nullptr;
       if constexpr (REL) {
         // the sub-tile's distances i - j run over dlo .. dlo + 62: row r of the scratch holds the
-        // terms of distance dlo + r, computed from the position rows of bucket(dlo + r), so a
-        // score's two terms sit at fixed offsets from per-lane bases (no bucket lookup per score)
+        // term of distance dlo + r, computed from the position row of bucket(dlo + r), so a
+        // score's term sits at a fixed offset from a per-lane base (no bucket lookup per score).
+        // Score (query q, key jl) is at distance row q + 31 - jl: c2p[q][q + 31 - jl] and
+        // p2c[jl][q + 31 - jl]. With jl = jc + 4 g (jc a constant per register) the lane's part
+        // goes into the base and each read has a constant, non-negative offset. The c2p term is
+        // added first, then the p2c term takes the same scratch (a wavefront's LDS operations
+        // run in order: its reads of the first term precede the second term's writes).
         const int kj0 = kb + kt * 32, qw0 = q0 + w * 32;
         const int dlo = qw0 - (kj0 + 31);
-        float *c2pw = sRel + (w * 2) * 32 * RP;
-        float *p2cw = c2pw + 32 * RP;
-        const int64_t hd = (int64_t)H * D;
+        float *sw = sRel + w * 32 * RP;
         const T *krow = &sK[(kt * 32 + (lane & 31)) * LDK + g * MF::KLANE];
+        auto term = [&](auto p2c_t) {
+          constexpr bool P2C = decltype(p2c_t)::value;
+          [[maybe_unused]] float16v c2p_lo;
+          if constexpr (!P2C) c2p_lo = c2p_block(dlo, std::true_type{});
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
-          int di = dlo + (lane & 31) + mt * 32 + a.lmax - 1;  // this lane's distance row
-          di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
-          const int pr = sBucket[di];  // < nb: the relidx table is checked against the tables
-          const T *pk = (const T *)a.pos_key + pr * hd + h * D + g * MF::KLANE;
-          const T *pq = (const T *)a.pos_query + pr * hd + h * D + g * MF::KLANE;
-          float16v cq = {}, ck = {};
+          for (int mt = 0; mt < 2; mt++) {
+            float16v c = {};
+            if constexpr (P2C) {
+              int di = dlo + (lane & 31) + mt * 32 + a.lmax - 1;  // this lane's distance row
+              di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
+              const int pr = sBucket[di];  // < nb: the relidx table is checked against the tables
+              const T *pt = (const T *)a.pos_query + pr * hd + h * D + g * MF::KLANE;
 #pragma unroll
-          for (int s = 0; s < QS; s++) {
-            typename MF::frag fk, fq, kf;
-            if constexpr (sizeof(T) == 2) {
-              fk = *reinterpret_cast<const half8v *>(pk + s * MF::KSTEP);
-              fq = *reinterpret_cast<const half8v *>(pq + s * MF::KSTEP);
-              kf = *reinterpret_cast<const half8v *>(krow + s * MF::KSTEP);
+              for (int s = 0; s < QS; s++) {
+                typename MF::frag fp, kf;
+                if constexpr (sizeof(T) == 2) {
+                  fp = *reinterpret_cast<const half8v *>(pt + s * MF::KSTEP);
+                  kf = *reinterpret_cast<const half8v *>(krow + s * MF::KSTEP);
+                } else {
+                  fp = pt[s * MF::KSTEP];
+                  kf = krow[s * MF::KSTEP];
+                }
+                c = MF::mma(fp, kf, c);  // [m][key]: lane = key
+              }
             } else {
-              fk = pk[s * MF::KSTEP];
-              fq = pq[s * MF::KSTEP];
-              kf = krow[s * MF::KSTEP];
+              c = mt == 0 ? c2p_lo : c2p_carry;  // [m][query]: lane = query
             }
-            cq = MF::mma(fk, qf[s], cq);  // [m][query]: lane = query
-            ck = MF::mma(fq, kf, ck);     // [m][key]: lane = key
-          }
-          // registers 4 r4 .. 4 r4 + 3 are distance rows 32 mt + 8 r4 + 4 g + {0..3}
+            // registers 4 r4 .. 4 r4 + 3 are distance rows 32 mt + 8 r4 + 4 g + {0..3}
 #pragma unroll
-          for (int r4 = 0; r4 < 4; r4++) {
-            const int mm = mt * 32 + 8 * r4 + 4 * g;
-            *reinterpret_cast<float4v *>(&c2pw[(lane & 31) * RP + mm]) =
-                float4v{cq[4 * r4], cq[4 * r4 + 1], cq[4 * r4 + 2], cq[4 * r4 + 3]};
-            *reinterpret_cast<float4v *>(&p2cw[(lane & 31) * RP + mm]) =
-                float4v{ck[4 * r4], ck[4 * r4 + 1], ck[4 * r4 + 2], ck[4 * r4 + 3]};
+            for (int r4 = 0; r4 < 4; r4++) {
+              const int mm = mt * 32 + 8 * r4 + 4 * g;
+              *reinterpret_cast<float4v *>(&sw[(lane & 31) * RP + mm]) =
+                  float4v{c[4 * r4], c[4 * r4 + 1], c[4 * r4 + 2], c[4 * r4 + 3]};
+            }
           }
-        }
-        // score (query q, key jl) is at distance row q + 31 - jl: c2p[q][q + 31 - jl] and
-        // p2c[jl][q + 31 - jl]. With jl = jc + 4 g (jc a constant per register) the lane's part
-        // goes into the bases and each read has a constant, non-negative offset.
-        c2pW = c2pw + (lane & 31) * (RP + 1) - 4 * g;
-        p2cW = p2cw + (lane & 31) + 31 + 4 * g * (RP - 1);
+          if constexpr (!P2C) c2p_carry = c2p_lo;
+          const float *base = P2C ? sw + (lane & 31) + 31 + 4 * g * (RP - 1) : sw + (lane & 31) * (RP + 1) - 4 * g;
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const int jc = 8 * (r >> 2) + (r & 3);
+            // read unconditionally (no branch per score); masked pairs are discarded below
+            sc[kt][r] = sc[kt][r] + (P2C ? base[jc * (RP - 1)] : base[31 - jc]);
+          }
+        };
+        term(std::false_type{});
+        term(std::true_type{});
       }
       const int k0 = kb + kt * 32;
       auto scores = [&](auto masked_t) {
@@ -237,12 +273,6 @@ attn_kernel(AttnArgs a, Packing p) {
         for (int r = 0; r < 16; r++) {
           const int jl = 8 * (r >> 2) + 4 * g + (r & 3);
           float v = sc[kt][r];
-          if constexpr (REL) {
-            // read unconditionally (no branch per score); masked pairs are discarded below
-            const int jc = 8 * (r >> 2) + (r & 3);
-            v = v + c2pW[31 - jc];
-            v = v + p2cW[jc * (RP - 1)];
-          }
           if constexpr (MASKED) {
             bool ok = jl < lim;
             if constexpr (WIN) ok = ok && jl >= wlo && jl <= whi;
@@ -252,9 +282,7 @@ attn_kernel(AttnArgs a, Packing p) {
           tmax = fmaxf(tmax, v);
         }
       };
-      // (the relative path keeps one masked body: two copies of its gathers cost more than the
-      // compares they save)
-      if (REL || WIN || k0 + 32 > khi) scores(std::true_type{});
+      if (WIN || k0 + 32 > khi) scores(std::true_type{});
       else scores(std::false_type{});
     }
     tmax = fmaxf(tmax, xor32(tmax));
@@ -354,8 +382,10 @@ attn_kernel(AttnArgs a, Packing p) {
 template <typename T, bool REL, bool WIN>
 void launch_w(const AttnArgs &a, const Packing &p, hipStream_t s) {
   dim3 grid((unsigned)(a.ntiles * a.H));
-  if (a.D == 64) launch((attn_kernel<T, 64, REL, WIN>), grid, dim3(128), 0, s, a, p);
-  else launch((attn_kernel<T, 32, REL, WIN>), grid, dim3(128), 0, s, a, p);
+  // the relative path's bucket table: 2 lmax - 1 16-bit entries of dynamic LDS
+  const unsigned dyn = REL ? (unsigned)((2 * a.lmax - 1) * sizeof(short) + 3) / 4 * 4 : 0;
+  if (a.D == 64) launch((attn_kernel<T, 64, REL, WIN>), grid, dim3(128), dyn, s, a, p);
+  else launch((attn_kernel<T, 32, REL, WIN>), grid, dim3(128), dyn, s, a, p);
 }
 
 template <typename T, bool REL>
