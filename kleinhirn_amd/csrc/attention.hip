@@ -54,12 +54,48 @@ struct AttnMfma<float> {
   }
 };
 
+// Head dimensions other than 32 and 64 (PAD): the kernel runs at D (the next of 32, 64) with the
+// columns a.D .. D - 1 read as zero (they add nothing to the products) and never stored; every
+// access is then element-wise, as the rows' head offsets h a.D need not be 16-byte aligned.
+template <typename T, bool PAD>
+__device__ __forceinline__ typename AttnMfma<T>::frag load_frag(const T *row, int d, int Dr) {
+  if constexpr (sizeof(T) == 2) {
+    if constexpr (!PAD) {
+      return *reinterpret_cast<const half8v *>(row + d);
+    } else {
+      half8v v;
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = d + e < Dr ? row[d + e] : (half_t)0;
+      return v;
+    }
+  } else {
+    if constexpr (!PAD) return row[d];
+    else return d < Dr ? row[d] : 0.f;
+  }
+}
+template <typename T, bool PAD>
+__device__ __forceinline__ uint4 load_chunk(const T *row, int d, int Dr) {
+  if constexpr (!PAD) {
+    return *reinterpret_cast<const uint4 *>(row + d);
+  } else {
+    constexpr int CE = 16 / sizeof(T);
+    T v[CE];
+#pragma unroll
+    for (int e = 0; e < CE; e++) v[e] = d + e < Dr ? row[d + e] : (T)0;
+    uint4 r;
+    __builtin_memcpy(&r, v, 16);
+    return r;
+  }
+}
+
 // Four wavefronts per SIMD on the standard path (short sequences are latency-bound), two on the
-// relative path. WIN: a sliding window (a.window > 0) bounds the keys of each query.
-template <typename T, int D, bool REL, bool WIN>
-__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(REL ? 2 : 4, 8)))
+// relative path (half of each with PAD, whose element-wise loads hold more registers). WIN: a
+// sliding window (a.window > 0) bounds the keys of each query.
+template <typename T, int D, bool REL, bool WIN, bool PAD>
+__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(PAD ? (REL ? 1 : 2) : (REL ? 2 : 4), 8)))
 attn_kernel(AttnArgs a, Packing p) {
   typedef AttnMfma<T> MF;
+  const int Dr = PAD ? a.D : D;           // the rows' head dimension
   constexpr int PADK = 16 / sizeof(T);   // 16 bytes of row padding
   constexpr int LDK = D + PADK;           // sK row
   // sVt row: 4 elements of padding (a 136-byte pitch for f16): the 4-key column writes of 8
@@ -85,7 +121,7 @@ attn_kernel(AttnArgs a, Packing p) {
   const int h = item / a.ntiles;
   const int64_t base = p.cu[b];
   const int n = p.cu[b + 1] - p.cu[b];
-  const int64_t rs = (int64_t)3 * H * D;  // qkv row stride
+  const int64_t rs = (int64_t)3 * H * Dr;  // qkv row stride
   const T *qkv = (const T *)a.qkv;
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -97,11 +133,7 @@ attn_kernel(AttnArgs a, Packing p) {
   // Q fragments: B operand of S^T = K Q^T (column = query, k = d)
   typename MF::frag qf[QS];
 #pragma unroll
-  for (int s = 0; s < QS; s++) {
-    const T *src = qkv + (base + qc) * rs + h * D + s * MF::KSTEP + g * MF::KLANE;
-    if constexpr (sizeof(T) == 2) qf[s] = *reinterpret_cast<const half8v *>(src);
-    else qf[s] = *src;
-  }
+  for (int s = 0; s < QS; s++) qf[s] = load_frag<T, PAD>(qkv + (base + qc) * rs + h * Dr, s * MF::KSTEP + g * MF::KLANE, Dr);
 
   // key range of this tile: the window around [q0, q0 + QT) or the whole sequence
   int klo = 0, khi = n;
@@ -119,22 +151,17 @@ attn_kernel(AttnArgs a, Packing p) {
   float m_run = -INFINITY, l_run = 0.f;
   // c2p rows of one 32-row distance block for this wavefront's queries: q . pos_key[bucket(d)]
   // for d = d0 + lane-row, as [row][query] accumulators (lane = query)
-  [[maybe_unused]] const int64_t hd = (int64_t)H * D;
+  const int64_t hd = (int64_t)H * Dr;
   // (the bucket table from LDS, or from global memory before the LDS copy is visible)
   [[maybe_unused]] auto c2p_block = [&](int d0, auto from_lds_t) {
     int di = d0 + (lane & 31) + a.lmax - 1;  // this lane's distance row
     di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
     // < nb: the relidx table is checked against the tables
     const int pr = decltype(from_lds_t)::value ? (int)sBucket[di] : a.bucket[di];
-    const T *pt = (const T *)a.pos_key + pr * hd + h * D + g * MF::KLANE;
+    const T *pt = (const T *)a.pos_key + pr * hd + h * Dr;
     float16v c = {};
 #pragma unroll
-    for (int s = 0; s < QS; s++) {
-      typename MF::frag fp;
-      if constexpr (sizeof(T) == 2) fp = *reinterpret_cast<const half8v *>(pt + s * MF::KSTEP);
-      else fp = pt[s * MF::KSTEP];
-      c = MF::mma(fp, qf[s], c);
-    }
+    for (int s = 0; s < QS; s++) c = MF::mma(load_frag<T, PAD>(pt, s * MF::KSTEP + g * MF::KLANE, Dr), qf[s], c);
     return c;
   };
   // The distance window of the sub-tile of keys kj0 .. kj0 + 31 starts at dlo = qw0 - kj0 - 31; the
@@ -161,8 +188,8 @@ attn_kernel(AttnArgs a, Packing p) {
         vv[u] = make_uint4(0, 0, 0, 0);
         if (j < khi) {
           const T *row = qkv + (base + j) * rs;
-          kv[u] = *reinterpret_cast<const uint4 *>(row + (H + h) * D + dc);
-          vv[u] = *reinterpret_cast<const uint4 *>(row + (2 * H + h) * D + dc);
+          kv[u] = load_chunk<T, PAD>(row + (H + h) * Dr, dc, Dr);
+          vv[u] = load_chunk<T, PAD>(row + (2 * H + h) * Dr, dc, Dr);
         }
       }
 #pragma unroll
@@ -228,18 +255,14 @@ attn_kernel(AttnArgs a, Packing p) {
               int di = dlo + (lane & 31) + mt * 32 + a.lmax - 1;  // this lane's distance row
               di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
               const int pr = sBucket[di];  // < nb: the relidx table is checked against the tables
-              const T *pt = (const T *)a.pos_query + pr * hd + h * D + g * MF::KLANE;
+              const T *pt = (const T *)a.pos_query + pr * hd + h * Dr;
 #pragma unroll
               for (int s = 0; s < QS; s++) {
-                typename MF::frag fp, kf;
-                if constexpr (sizeof(T) == 2) {
-                  fp = *reinterpret_cast<const half8v *>(pt + s * MF::KSTEP);
-                  kf = *reinterpret_cast<const half8v *>(krow + s * MF::KSTEP);
-                } else {
-                  fp = pt[s * MF::KSTEP];
-                  kf = krow[s * MF::KSTEP];
-                }
-                c = MF::mma(fp, kf, c);  // [m][key]: lane = key
+                typename MF::frag kf;
+                if constexpr (sizeof(T) == 2) kf = *reinterpret_cast<const half8v *>(krow + s * MF::KSTEP);
+                else kf = krow[s * MF::KSTEP];
+                // [m][key]: lane = key
+                c = MF::mma(load_frag<T, PAD>(pt, s * MF::KSTEP + g * MF::KLANE, Dr), kf, c);
               }
             } else {
               c = mt == 0 ? c2p_lo : c2p_carry;  // [m][query]: lane = query
@@ -372,10 +395,16 @@ attn_kernel(AttnArgs a, Packing p) {
   __syncthreads();
   // rows of queries past the sequence (clamped lanes) stay in LDS
   const int rows = n - q0 < QT ? n - q0 : QT;
-  T *out = (T *)a.ctx + base * (int64_t)H * D + h * D;
+  T *out = (T *)a.ctx + base * hd + h * Dr;
   for (int c = t; c < rows * CPR; c += 128) {
     const int r = c / CPR, dc = (c % CPR) * CE;
-    *reinterpret_cast<uint4 *>(out + (int64_t)(q0 + r) * H * D + dc) = *reinterpret_cast<const uint4 *>(sO + r * LDO + dc);
+    if constexpr (!PAD) {
+      *reinterpret_cast<uint4 *>(out + (int64_t)(q0 + r) * hd + dc) = *reinterpret_cast<const uint4 *>(sO + r * LDO + dc);
+    } else {
+#pragma unroll
+      for (int e = 0; e < CE; e++)
+        if (dc + e < Dr) out[(int64_t)(q0 + r) * hd + dc + e] = sO[r * LDO + dc + e];
+    }
   }
 }
 
@@ -384,8 +413,11 @@ void launch_w(const AttnArgs &a, const Packing &p, hipStream_t s) {
   dim3 grid((unsigned)(a.ntiles * a.H));
   // the relative path's bucket table: 2 lmax - 1 16-bit entries of dynamic LDS
   const unsigned dyn = REL ? (unsigned)((2 * a.lmax - 1) * sizeof(short) + 3) / 4 * 4 : 0;
-  if (a.D == 64) launch((attn_kernel<T, 64, REL, WIN>), grid, dim3(128), dyn, s, a, p);
-  else launch((attn_kernel<T, 32, REL, WIN>), grid, dim3(128), dyn, s, a, p);
+  // head dimensions 32 and 64 as they are; others padded to the next of the two (up to 64)
+  if (a.D == 64) launch((attn_kernel<T, 64, REL, WIN, false>), grid, dim3(128), dyn, s, a, p);
+  else if (a.D == 32) launch((attn_kernel<T, 32, REL, WIN, false>), grid, dim3(128), dyn, s, a, p);
+  else if (a.D < 32) launch((attn_kernel<T, 32, REL, WIN, true>), grid, dim3(128), dyn, s, a, p);
+  else launch((attn_kernel<T, 64, REL, WIN, true>), grid, dim3(128), dyn, s, a, p);
 }
 
 template <typename T, bool REL>

@@ -133,6 +133,7 @@ struct AttnArgs {
 };
 void attention(bool f16, const AttnArgs &a, const Packing &p, hipStream_t s);
 constexpr int ATTN_QTILE = 64;
+constexpr int ATTN_DMAX = 64;  // largest head dimension (32 and 64 run as they are, others padded)
 constexpr int ATTN_REL_LMAX = 2048;  // longest plan the relative attention kernel takes (its LDS bucket table)
 
 // Row 0 of each sequence into one row per sequence (from_packed), or one row per sequence copied

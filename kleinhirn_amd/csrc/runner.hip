@@ -444,8 +444,9 @@ static std::vector<Step> lower(const Parsed &pp, bool f16, int L, std::vector<st
         fail(KH_EUNSUPPORTED, "kernel " + kn + " has no HIP computation (outside the encoder heads)");
       }
       if (s.kind == S_ATTN) {
-        if (s.D != 32 && s.D != 64)
-          fail(KH_EUNSUPPORTED, "attention head dimension " + std::to_string(s.D) + " (32 or 64 supported)");
+        if (s.D < 1 || s.D > ATTN_DMAX)
+          fail(KH_EUNSUPPORTED, "attention head dimension " + std::to_string(s.D) + " (1 .. " +
+                                    std::to_string(ATTN_DMAX) + " supported)");
       }
       steps.push_back(std::move(s));
     } catch (const Error &e) {

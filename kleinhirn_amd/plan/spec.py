@@ -138,6 +138,23 @@ def deberta_v3(hidden: int, layers: int, heads: int, intermediate: int, vocab: i
     }
 
 
+def deberta_v2_absolute(hidden: int, layers: int, heads: int, intermediate: int, vocab: int,
+                        max_positions: int = 512, eps: float = 1e-7, act: str = "gelu") -> dict:
+    """DeBERTa-v2 without relative attention (src/plan/hf.ts:327-345, polyBERT): absolute positions
+    added before the embedding LayerNorm, the standard attention, the embeddings times the mask."""
+    head_dim = hidden // heads
+    norm = {"eps": eps, "bias": True}
+    return {
+        "family": "deberta-v2", "hidden": hidden, "layers": layers, "heads": heads,
+        "headDim": head_dim, "intermediate": intermediate, "vocab": vocab, "embeddingSize": hidden,
+        "embed": {"positions": "absolute", "positionOffset": 0, "maxPositions": max_positions, "typeVocab": 0,
+                  "norm": norm, "maskMultiply": True, "project": False},
+        "attention": {"kind": "standard", "bias": True, "scale": head_dim ** -0.5},
+        "block": {"order": "post", "firstNormIdentity": False, "finalNorm": False, "norm": norm},
+        "ffn": {"kind": "mlp", "act": act, "bias": True},
+    }
+
+
 def gliner(enc: dict, temperature: float, head_hidden: int | None = None, markers: int = 16) -> tuple[dict, dict]:
     """specFromGlinerManifest (src/plan/spec.ts:214-246): the DeBERTa-v2 encoder of a GLiNER2
     manifest (relative c2p+p2c attention, embedding LayerNorm times the mask, no position or type
@@ -256,7 +273,7 @@ def manifest_tensors(spec: dict, head: dict) -> list[tuple[str, tuple[int, ...],
         ):
             if t.get(key):
                 out.append((t[key], shape, kind))
-        if t.get("posKey"):
+        if t.get("posKey") and spec["attention"]["kind"] == "deberta-relative":
             rows = 2 * spec["attention"]["rel"]["buckets"]
             out.append((t["posKey"], (rows, H), "rel"))
             out.append((t["posQuery"], (rows, H), "rel"))

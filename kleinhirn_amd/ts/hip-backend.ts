@@ -138,6 +138,23 @@ export class HipPlanRunner implements PlanRunner {
     this.kh.upload(this.handle(), input.embeddings, input.mask, input.typeIds ?? null);
   }
 
+  // The same run by token ids instead of embedding rows: the rows come from the device word table
+  // (HipBackend.setWords, or the words of loadManifest) on the GPU (kh_upload_ids). ids holds
+  // length x batch entries laid out as the mask (entries under mask 0 are not read).
+  uploadIds(ids: Int32Array, mask: Float32Array, typeIds?: Uint32Array | null,
+    extra: Pick<RunInput, 'packedMarkers' | 'qtype'> = {}): void {
+    if (this.plan.inputs.markers) {
+      if (!extra.packedMarkers) throw new Error('plan needs packedMarkers');
+      this.kh.uploadMarkers(this.handle(), extra.packedMarkers);
+    }
+    if (this.plan.rowSelect) {
+      const q = Array.isArray(extra.qtype) ? extra.qtype : [extra.qtype ?? 0];
+      this.kh.uploadQtypes(this.handle(), Uint32Array.from(q));
+    }
+    if (this.plan.inputs.typeIds && !typeIds) throw new Error('plan needs typeIds');
+    this.kh.uploadIds(this.handle(), ids, mask, typeIds ?? null);
+  }
+
   run(seqLen: number, capture?: boolean): void {
     if (capture) this.assertCapturable();
     this.kh.run(this.handle(), seqLen);
@@ -167,8 +184,9 @@ export class HipPlanRunner implements PlanRunner {
 }
 
 export class HipBackend implements Backend {
-  // Backend.kind is 'webgpu' | 'wasm' in src/backend.ts:31; the HIP seam widens it
-  readonly kind = 'hip' as unknown as 'wasm';
+  // Backend.kind widened to 'webgpu' | 'wasm' | 'hip' (the one-line edit of src/backend.ts:31 this
+  // backend comes with); without it this line does not type-check, by design
+  readonly kind = 'hip' as const;
   private ctx: KhHandle | undefined;
 
   constructor(private kh: KhAddon, device = 0) {
@@ -204,7 +222,7 @@ export class HipBackend implements Backend {
     this.kh.planCheck(this.context(), planJson(plan));
   }
 
-  runner(plan: Plan): PlanRunner {
+  runner(plan: Plan): HipPlanRunner {
     return new HipPlanRunner(this.kh, this.context(), plan);
   }
 

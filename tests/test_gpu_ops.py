@@ -211,8 +211,11 @@ def attention_ref(qkv, lens, L, H, D, scale, window=0, rel=None):
 
 @pytest.mark.parametrize("f16", [False, True])
 @pytest.mark.parametrize("D,lens,window,split", [(64, [5, 70], 0, True), (32, [128], 0, False), (64, [200, 3], 2, True),
-                                                 (64, [300], 64, False), (32, [1, 65, 64], 0, True)])
+                                                 (64, [300], 64, False), (32, [1, 65, 64], 0, True),
+                                                 (50, [5, 70], 0, True), (20, [33, 1], 0, False),
+                                                 (40, [150], 64, False)])
 def test_standard_attention(f16, D, lens, window, split):
+    """Head dimensions 32 and 64, and others (50 as polyBERT's, 20, 40) padded inside the kernel."""
     H = 3
     L = max(lens)
     L = ((L + 31) // 32) * 32
@@ -243,9 +246,10 @@ def test_standard_attention(f16, D, lens, window, split):
 
 
 @pytest.mark.parametrize("f16", [False, True])
-@pytest.mark.parametrize("lens,split", [([7], False), ([40, 129], True), ([200], False)])
-def test_relative_attention(f16, lens, split):
-    H, D = 2, 64
+@pytest.mark.parametrize("D,lens,split", [(64, [7], False), (64, [40, 129], True), (64, [200], False),
+                                          (50, [90, 33], False), (50, [70], True)])
+def test_relative_attention(f16, D, lens, split):
+    H = 2
     L = 256
     B = len(lens)
     hd = H * D
