@@ -73,6 +73,19 @@ struct Packing {
   int64_t T;
 };
 
+
+// Ranges (16-byte pieces) a LayerNorm launch reads and discards after its rows: the weights of the
+// products that follow it, brought into the memory-side cache just before they run. total is the
+// sum of n16; sink is a device word the kernels never write (never is 0).
+constexpr int PREFETCH_RANGES = 4;
+struct PrefetchArgs {
+  const void *p[PREFETCH_RANGES] = {};
+  int64_t n16[PREFETCH_RANGES] = {};
+  int64_t total = 0;
+  uint32_t *sink = nullptr;
+  int never = 0;
+};
+
 struct EmbLnArgs {
   const void *word = nullptr;    // packed word rows [T, N], or null with table + ids
   const void *table = nullptr;   // device word table [rows, N]
@@ -85,7 +98,7 @@ struct EmbLnArgs {
   int N = 0, offset = 0, maxpos = 1, posids = 0;
   float eps = 0.f;
 };
-void embln(bool f16, const EmbLnArgs &a, const Packing &p, hipStream_t s);
+void embln(bool f16, const EmbLnArgs &a, const Packing &p, hipStream_t s, const PrefetchArgs &pf = PrefetchArgs());
 
 // GLiNER2 logits: logits[k] = raw[k] / temp where marker k's mask word (f32 bits at
 // b * 3K + K + k mod K of the packed payloads, b = k / K) exceeds 0.5, else -1e4; total = B * K.
@@ -95,7 +108,8 @@ void mask_logits(bool f16, const void *raw, const uint32_t *packed, float *logit
 // LN over rows: MODE 2 adds b first. rows = T (packed) or B (sequence rows). With ids, row r is
 // row ids[r] of a (the device word table), with the arithmetic of the same LN over gathered rows.
 void layernorm(bool f16, const void *a, const void *b, const void *gamma, const void *beta, void *out,
-               int64_t rows, int N, float eps, hipStream_t s, const int32_t *ids = nullptr);
+               int64_t rows, int N, float eps, hipStream_t s, const int32_t *ids = nullptr,
+               const PrefetchArgs &pf = PrefetchArgs());
 
 // dst += src (MODE 0) or dst[r] += src[seq(r)] (MODE 1), rounded to storage.
 void add(bool f16, void *dst, const void *src, int64_t rows, int N, int mode, const Packing &p,

@@ -14,6 +14,28 @@ namespace {
 
 constexpr int ROWS_PER_BLOCK = 4;  // wavefronts (rows) per 256-thread block
 
+// The weight prefetch a LayerNorm launch carries (PrefetchArgs): after its rows are stored, every
+// thread of the grid reads its share of the ranges' 16-byte pieces (piece g, g + threads, ...), so
+// the reads wait on nothing and the launch ends about one memory latency later. The XOR of the
+// words is stored only when `never` is set, which the host never does; the compiler cannot drop
+// the loads.
+__device__ __forceinline__ void prefetch_share(const PrefetchArgs &pf) {
+  if (pf.total <= 0) return;
+  const int64_t nth = (int64_t)gridDim.x * blockDim.x;
+  uint32_t acc = 0;
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < pf.total; g += nth) {
+    int64_t off = g;
+    int r = 0;
+    while (r < PREFETCH_RANGES - 1 && off >= pf.n16[r]) {
+      off -= pf.n16[r];
+      r++;
+    }
+    const uint4 v = ((const uint4 *)pf.p[r])[off];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (pf.never) pf.sink[0] = acc;
+}
+
 // Per lane: PER groups of VEC contiguous elements; group g = k * 64 + lane.
 template <typename T, int VEC, int PER>
 __device__ __forceinline__ void ln_finish(float (&v)[PER][VEC], int N, const T *gamma, const T *beta,
@@ -55,10 +77,13 @@ template <typename T, int VEC, int PER>
 __global__ void __launch_bounds__(256) layernorm_kernel(const T *__restrict__ a, const T *__restrict__ b,
                                                         const T *__restrict__ gamma, const T *__restrict__ beta,
                                                         T *__restrict__ out, int64_t rows, int N, float eps,
-                                                        const int32_t *__restrict__ ids) {
+                                                        const int32_t *__restrict__ ids, PrefetchArgs pf) {
   int lane = threadIdx.x & 63;
   int64_t r = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
-  if (r >= rows) return;
+  if (r >= rows) {
+    prefetch_share(pf);
+    return;
+  }
   const T *ar = a + (ids ? (int64_t)ids[r] : r) * N;
   const T *br = b ? b + r * N : nullptr;
   float v[PER][VEC];
@@ -79,6 +104,7 @@ __global__ void __launch_bounds__(256) layernorm_kernel(const T *__restrict__ a,
     }
   }
   ln_finish<T, VEC, PER>(v, N, gamma, beta, eps, out + r * N, lane);
+  prefetch_share(pf);
 }
 
 
@@ -90,12 +116,15 @@ __global__ void __launch_bounds__(256) layernorm_rows_kernel(const T *__restrict
                                                              const T *__restrict__ gamma,
                                                              const T *__restrict__ beta, T *__restrict__ out,
                                                              int64_t rows, int N, float eps,
-                                                             const int32_t *__restrict__ ids) {
+                                                             const int32_t *__restrict__ ids, PrefetchArgs pf) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int RPW = WAVE / LPR;  // rows per wavefront
   const int lane = threadIdx.x & 63, l = lane % LPR;
   const int64_t r = ((int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6)) * RPW + lane / LPR;
-  if (r >= rows) return;  // whole groups leave together: the shuffles below stay in a group
+  if (r >= rows) {  // whole groups leave together: the shuffles below stay in a group
+    prefetch_share(pf);
+    return;
+  }
   const T *ar = a + (ids ? (int64_t)ids[r] : r) * N;
   float v[PER][VEC];
 #pragma unroll
@@ -140,16 +169,20 @@ __global__ void __launch_bounds__(256) layernorm_rows_kernel(const T *__restrict
     for (int i = 0; i < VEC; i++) y[i] = (v[k][i] - mean) * inv * gm[i] + (beta ? bt[i] : 0.f);
     VecIO<T, VEC>::store(out + r * N + e0, y);
   }
+  prefetch_share(pf);
 }
 
 // word + position + type in f32 ((word + pos) + type), then LayerNorm (src/wasm/plan.ts:433-447).
 // Position row: tt >> 16 with POSIDS, else the row's position in its sequence + OFFSET, clamped to
 // MAXPOS - 1. Type row: tt & 0xffff.
 template <typename T, int VEC, int PER>
-__global__ void __launch_bounds__(256) embln_kernel(EmbLnArgs a, Packing p) {
+__global__ void __launch_bounds__(256) embln_kernel(EmbLnArgs a, Packing p, PrefetchArgs pf) {
   int lane = threadIdx.x & 63;
   int64_t r = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
-  if (r >= p.T) return;
+  if (r >= p.T) {
+    prefetch_share(pf);
+    return;
+  }
   const int N = a.N;
   uint32_t t = a.tt ? a.tt[r] : 0u;
   int prow = a.posids ? (int)(t >> 16) : p.row_pos[r] + a.offset;
@@ -174,6 +207,7 @@ __global__ void __launch_bounds__(256) embln_kernel(EmbLnArgs a, Packing p) {
     }
   }
   ln_finish<T, VEC, PER>(v, N, (const T *)a.gamma, (const T *)a.beta, a.eps, (T *)a.out + r * N, lane);
+  prefetch_share(pf);
 }
 
 template <typename T, int VEC>
@@ -202,7 +236,7 @@ bool dispatch_per(int N, F &&f) {
 
 template <typename T>
 void layernorm_t(const void *a, const void *b, const void *gamma, const void *beta, void *out, int64_t rows,
-                 int N, float eps, const int32_t *ids, hipStream_t s) {
+                 int N, float eps, const int32_t *ids, const PrefetchArgs &pf, hipStream_t s) {
   // rows of 3 x 2^j 16-byte chunks (384- and 768-wide f16, 384-wide f32): groups of 2^j lanes
   constexpr int VEC16 = 16 / sizeof(T);
   if (N % (3 * VEC16) == 0) {
@@ -211,7 +245,7 @@ void layernorm_t(const void *a, const void *b, const void *gamma, const void *be
       constexpr int LPR = decltype(lpr_t)::value;
       const int64_t per_block = (int64_t)ROWS_PER_BLOCK * (WAVE / LPR);
       launch((layernorm_rows_kernel<T, LPR, 3>), dim3((unsigned)((rows + per_block - 1) / per_block)), dim3(256),
-             0, s, (const T *)a, (const T *)b, (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps, ids);
+             0, s, (const T *)a, (const T *)b, (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps, ids, pf);
     };
     switch (lpr) {
       case 8: go_rows(std::integral_constant<int, 8>()); return;
@@ -227,7 +261,7 @@ void layernorm_t(const void *a, const void *b, const void *gamma, const void *be
     dispatch_per<T, VEC>(N, [&](auto per) {
       constexpr int PER = decltype(per)::value;
       launch((layernorm_kernel<T, VEC, PER>), grid, dim3(256), 0, s, (const T *)a, (const T *)b,
-                         (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps, ids);
+                         (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps, ids, pf);
     });
   };
   // 16-byte loads where the width allows
@@ -238,13 +272,13 @@ void layernorm_t(const void *a, const void *b, const void *gamma, const void *be
 }
 
 template <typename T>
-void embln_t(const EmbLnArgs &a, const Packing &p, hipStream_t s) {
+void embln_t(const EmbLnArgs &a, const Packing &p, const PrefetchArgs &pf, hipStream_t s) {
   dim3 grid((unsigned)((p.T + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK));
   auto go = [&](auto vec) {
     constexpr int VEC = decltype(vec)::value;
     dispatch_per<T, VEC>(a.N, [&](auto per) {
       constexpr int PER = decltype(per)::value;
-      launch((embln_kernel<T, VEC, PER>), grid, dim3(256), 0, s, a, p);
+      launch((embln_kernel<T, VEC, PER>), grid, dim3(256), 0, s, a, p, pf);
     });
   };
   if (a.N % (16 / sizeof(T)) == 0) go(std::integral_constant<int, 16 / sizeof(T)>());
@@ -413,16 +447,16 @@ void first_rows(bool f16, const void *src, void *dst, int D, bool from_packed, c
 }
 
 void layernorm(bool f16, const void *a, const void *b, const void *gamma, const void *beta, void *out,
-               int64_t rows, int N, float eps, hipStream_t s, const int32_t *ids) {
+               int64_t rows, int N, float eps, hipStream_t s, const int32_t *ids, const PrefetchArgs &pf) {
   if (rows <= 0) return;
-  if (f16) layernorm_t<half_t>(a, b, gamma, beta, out, rows, N, eps, ids, s);
-  else layernorm_t<float>(a, b, gamma, beta, out, rows, N, eps, ids, s);
+  if (f16) layernorm_t<half_t>(a, b, gamma, beta, out, rows, N, eps, ids, pf, s);
+  else layernorm_t<float>(a, b, gamma, beta, out, rows, N, eps, ids, pf, s);
 }
 
-void embln(bool f16, const EmbLnArgs &a, const Packing &p, hipStream_t s) {
+void embln(bool f16, const EmbLnArgs &a, const Packing &p, hipStream_t s, const PrefetchArgs &pf) {
   if (p.T <= 0) return;
-  if (f16) embln_t<half_t>(a, p, s);
-  else embln_t<float>(a, p, s);
+  if (f16) embln_t<half_t>(a, p, pf, s);
+  else embln_t<float>(a, p, pf, s);
 }
 
 void add(bool f16, void *dst, const void *src, int64_t rows, int N, int mode, const Packing &p, hipStream_t s) {

@@ -197,6 +197,8 @@ struct kh_plan {
   hipStream_t stream = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   bool ran = false;
+  // the never-written word of the LayerNorm kernels' weight prefetch
+  DevMem pf_sink;
 
   // A small batch runs as two halves on two streams: sequences [0, split) here, [split, B) on the
   // twin (the same plan, its own buffers and stream), so the kernels of one half fill the CUs the
@@ -771,7 +773,7 @@ using LaunchHook = std::function<void(const Step &, const char *kernel, double f
 
 static void *bufp(kh_plan *pl, const Ref &r) { return r.p; }
 
-static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
+static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook, const PrefetchArgs &pf) {
   hipStream_t st = pl->stream;
   const bool f16 = pl->f16;
   const size_t es = f16 ? 2 : 4;
@@ -824,14 +826,14 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
         // table, so the result equals the LN of the uploaded rows bit for bit
         begin("layernorm", 8.0 * pl->T * s.N, 2.0 * es * pl->T * s.N + 4.0 * pl->T);
         layernorm(f16, pl->ctx->words->p, nullptr, bufp(pl, s.in[2]), bufp(pl, s.in[3]), bufp(pl, s.in[5]), pl->T,
-                  s.N, s.eps, st, (const int32_t *)pl->d_ids.p);
+                  s.N, s.eps, st, (const int32_t *)pl->d_ids.p, pf);
         end();
         break;
       }
       const void *b = s.mode == 2 ? bufp(pl, s.in[1]) : nullptr;
       begin("layernorm", 8.0 * rows * s.N, (double)es * ((s.mode == 2 ? 3.0 : 2.0) * rows * s.N + 2.0 * s.N));
       layernorm(f16, bufp(pl, s.in[0]), b, bufp(pl, s.in[2]), bufp(pl, s.in[3]), bufp(pl, s.in[5]), rows, s.N, s.eps,
-                st);
+                st, nullptr, pf);
       end();
       break;
     }
@@ -853,7 +855,7 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook) {
       a.eps = s.eps;
       const int tables = 1 + (a.pos ? 1 : 0) + (a.typ ? 1 : 0);
       begin("embln", 9.0 * pl->T * s.N, (double)es * (tables + 1.0) * pl->T * s.N + 4.0 * pl->T);
-      embln(f16, a, pk, st);
+      embln(f16, a, pk, st, pf);
       end();
       break;
     }
@@ -1120,8 +1122,47 @@ static void ensure_rel(kh_plan *pl) {
   if (!pl->d_bucket.p) fail(KH_EINVAL, "relative attention needs the relidx table (kh_plan_init_buffer)");
 }
 
+static int64_t env_int(const char *name, int64_t dflt);
+
+// bytes of a product's weight matrix worth a prefetch (below this the product's own first reads
+// are a small part of it)
+constexpr size_t PREFETCH_MIN = 256 * 1024;
+
+// A LayerNorm over the packed rows carries the weights of the products up to the next LayerNorm
+// (PrefetchArgs: its threads read them after their rows), so those products find them in the
+// memory-side cache: a layer's weights come cold from HBM otherwise, which costs a product up to
+// a quarter of its time when the weights are a sizeable part of its operands (c2: 14 MB of
+// weights per layer against 20 MB rows). Products whose weights are under an eighth of their row
+// operand (c4, c5) gain nothing and are left out.
+static PrefetchArgs prefetch_for(kh_plan *pl, const std::vector<Step> &steps, size_t i) {
+  PrefetchArgs a;
+  int r = 0;
+  for (size_t j = i + 1; j < steps.size() && r < PREFETCH_RANGES; j++) {
+    const Step &s = steps[j];
+    if (s.kind == S_LN || s.kind == S_EMBLN) break;
+    if (s.kind != S_GEMM || s.seq_rows) continue;
+    const size_t es = pl->f16 ? 2 : 4;
+    const size_t bytes = (size_t)s.N * s.K * es;
+    if (bytes < PREFETCH_MIN || bytes * 8 < (size_t)pl->T * s.K * es) continue;
+    a.p[r] = bufp(pl, s.in[1]);
+    a.n16[r] = (int64_t)(bytes / 16);
+    a.total += a.n16[r];
+    r++;
+  }
+  if (r > 0) {
+    if (!pl->pf_sink.p) pl->pf_sink.alloc(256);
+    a.sink = (uint32_t *)pl->pf_sink.p;
+  }
+  return a;
+}
+
 static void run_steps(kh_plan *pl, const LaunchHook &hook) {
-  for (const Step &s : active_steps(pl)) exec_step(pl, s, hook);
+  const std::vector<Step> &steps = active_steps(pl);
+  const bool pf = env_int("KH_NO_PREFETCH", 0) == 0;
+  for (size_t i = 0; i < steps.size(); i++) {
+    const bool ln = (steps[i].kind == S_LN || steps[i].kind == S_EMBLN) && !steps[i].seq_rows;
+    exec_step(pl, steps[i], hook, pf && ln ? prefetch_for(pl, steps, i) : PrefetchArgs());
+  }
   KH_CHECK(hipGetLastError());
 }
 

@@ -37,6 +37,7 @@ FAMILIES = [
     ("pool_kernel", "pool"),
     ("gather_kernel", "gather"),
     ("first_rows_kernel", "compact"),
+    ("prefetch_kernel", "prefetch"),
     ("to_f32_kernel", "to_f32"),
     ("elementwise_kernel", "probe_copy"),
     ("copyBuffer", "runtime_copy"),
