@@ -116,11 +116,11 @@ attn_kernel(AttnArgs a, Packing p) {
   // together on one XCD and find its K and V rows in that XCD's L2
   const int H = a.H;
   const int item = xcd_tile(blockIdx.x, a.ntiles * H);
-  const int2 tile = a.tiles[item % a.ntiles];
-  const int b = tile.x, q0 = tile.y;
+  const int4 tile = a.tiles[item % a.ntiles];
+  const int q0 = tile.y;
   const int h = item / a.ntiles;
-  const int64_t base = p.cu[b];
-  const int n = p.cu[b + 1] - p.cu[b];
+  const int64_t base = tile.z;
+  const int n = tile.w;
   const int64_t rs = (int64_t)3 * H * Dr;  // qkv row stride
   const T *qkv = (const T *)a.qkv;
 

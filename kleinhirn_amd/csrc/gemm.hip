@@ -943,7 +943,7 @@ static int64_t lean_cost(const GemmArgs &g, int bm, int bn) {
 // Tile configurations. Lean f16 kernel: 8 = 192x128 (4 wavefronts of 96x64, two blocks per CU),
 // 9 = 192x256 (8 wavefronts of 96x64), 10 = 128x128 (4 of 64x64), 11 = 64x64 (1), 12 = 128x384
 // (8 of 64x96), 13 = 64x64 (4 of 32x32) with 8 slab stages, 7 slabs in flight (a few hundred rows:
-// the slab chain is the latency). DMA kernel: 0 = 256x256 (8 of
+// the slab chain is the latency), 14 = 256x256 (8 of 128x64). DMA kernel: 0 = 256x256 (8 of
 // 128x64, 2 stages), 1 = 256x128 (4 of 128x64, 3 stages), 2 = 128x128 (4 of 64x64, 4 stages),
 // 3 = 128x128 (4 of 64x64, 2 stages, two blocks per CU), 4 = 256x256 (4 of 128x128); persistent
 // 5/6/7. KH_GEMM_TILE forces one (tuning runs).
@@ -951,13 +951,19 @@ int pick_tile(const GemmArgs &g, bool lean) {
   const char *e = getenv("KH_GEMM_TILE");
   const int forced = e ? atoi(e) : -1;
   // (a fused step runs in the lean kernel only)
-  if (forced >= 0 && forced <= 13 && (forced < 8 ? g.epi == EPI_NONE : lean)) return forced;
+  if (forced >= 0 && forced <= 14 && (forced < 8 ? g.epi == EPI_NONE : lean)) return forced;
   // measured on MI355X (f16, random data, encoder shapes M = 13k .. 1.2M): 192x128 leads in
   // general; 192x256 where N is a multiple of 256 and either narrow (N <= 768: one round of tiles
   // at M ~ 13k) or fed by a short K (<= 384, where the epilogue weighs most)
   // (a few hundred rows, e.g. a pooled head: 64 x 64 tiles, enough of them to spread over CUs)
   if (lean) {
     if (g.M <= 1024) return 13;
+    // 256 x 256 (8 wavefronts of 128 x 64, one block per CU): 131 flop per loaded byte against
+    // 78 for 192 x 128, so the k loop is no longer bound by the loads into LDS. It wins where the
+    // product's K is short (<= 768) and the rows are many (c5's products +5-7 % each, c5 +2 % end
+    // to end). At c2's size (and its two halves of ~6,400 rows on two streams) one block per CU
+    // fills the chip worse than two of 192 x 128: c2 lost 1.6 % with it on the QKV product.
+    if (g.K <= 768 && g.M >= 65536) return 14;
     // very many rows (c5's 1.2M): per-tile efficiency decides, measured on the 384-wide models:
     // 128 x 384 for 384- and 768-wide outputs (one column tile: each A band is read once), 192 x 256
     // for wider ones fed by a short K
@@ -994,6 +1000,7 @@ void launch_act(const GemmArgs &g, hipStream_t s) {
       case 11: launch_lean<64, 64, 1, 1, ACT>(g, s); return;
       case 12: launch_lean<128, 384, 2, 4, ACT>(g, s); return;
       case 13: launch_lean<64, 64, 2, 2, ACT, 8>(g, s); return;
+      case 14: launch_lean<256, 256, 2, 4, ACT>(g, s); return;
       default: break;
     }
   }

@@ -128,7 +128,8 @@ void gather_rows(bool f16, const void *x, const uint32_t *markers, void *states,
                  const Packing &p, hipStream_t s);
 
 // Standard attention over packed rows: ctx = softmax(scale q k^T, window) v per (sequence, head).
-// tiles: [ntiles] (sequence, first query) pairs of 64-query tiles.
+// tiles: [ntiles] 64-query tiles as (sequence, first query, first packed row of the sequence,
+// sequence length), so a block needs no second lookup of cu_seqlens.
 struct AttnArgs {
   const void *qkv = nullptr;  // [T, 3 H D]
   void *ctx = nullptr;        // [T, H D]
@@ -142,7 +143,7 @@ struct AttnArgs {
   const int32_t *bucket = nullptr;  // [2 lmax - 1]
   int nb = 0;
   int lmax = 0;
-  const int2 *tiles;
+  const int4 *tiles;
   int ntiles;
 };
 void attention(bool f16, const AttnArgs &a, const Packing &p, hipStream_t s);

@@ -910,7 +910,7 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook, const 
       a.D = s.D;
       a.scale = s.scale;
       a.window = s.window;
-      a.tiles = (const int2 *)(s.first_tiles ? pl->d_tiles_first.p : pl->d_tiles.p);
+      a.tiles = (const int4 *)(s.first_tiles ? pl->d_tiles_first.p : pl->d_tiles.p);
       a.ntiles = s.first_tiles ? pl->ntiles_first : pl->ntiles;
       const double hd = (double)s.H * s.D;
       double pairs = s.first_tiles ? pl->attn_pairs_first : pl->attn_pairs_global;
@@ -962,9 +962,9 @@ static void pack(kh_plan *pl, int rows, int b_end) {
   const int64_t T = pl->cu[B];
   pl->T = T;
   std::vector<int32_t> row_pos(T > 0 ? T : 1), row_seq(T > 0 ? T : 1);
-  std::vector<int2> tiles;
+  std::vector<int4> tiles;
   pl->attn_pairs_global = 0;
-  std::vector<int2> tiles_first;
+  std::vector<int4> tiles_first;
   std::set<int> windows;
   for (const Step &s : pl->steps)
     if (s.kind == S_ATTN && s.window > 0) windows.insert(s.window);
@@ -977,9 +977,9 @@ static void pack(kh_plan *pl, int rows, int b_end) {
       row_pos[pl->cu[b] + i] = i;
       row_seq[pl->cu[b] + i] = b;
     }
-    for (int q = 0; q < n[b]; q += ATTN_QTILE) tiles.push_back(make_int2(b, q));
+    for (int q = 0; q < n[b]; q += ATTN_QTILE) tiles.push_back(make_int4(b, q, pl->cu[b], n[b]));
     const int nq = std::min(n[b], ATTN_QTILE);
-    if (n[b] > 0) tiles_first.push_back(make_int2(b, 0));
+    if (n[b] > 0) tiles_first.push_back(make_int4(b, 0, pl->cu[b], n[b]));
     pl->rows_first += nq;
     pl->attn_pairs_global += (double)n[b] * n[b];
     pl->attn_pairs_first += (double)nq * n[b];
@@ -1008,22 +1008,22 @@ static void pack(kh_plan *pl, int rows, int b_end) {
         // first tile: c2p over its query rows, p2c over every key row
         pl->rel_rows_buckets_first += 0.5 * (std::min(n[b], ATTN_QTILE) + n[b]) * range;
       }
-  if (tiles.empty()) tiles.push_back(make_int2(0, 0));
-  if (tiles_first.empty()) tiles_first.push_back(make_int2(0, 0));
+  if (tiles.empty()) tiles.push_back(make_int4(0, 0, 0, 0));
+  if (tiles_first.empty()) tiles_first.push_back(make_int4(0, 0, 0, 0));
 
   // metadata: cu | row_pos | row_seq | tiles | tt | ids, one pinned staging block
   const size_t es = pl->f16 ? 2 : 4;
   if (pl->d_cu.bytes < (size_t)(B + 1) * 4 || !pl->d_cu.p) pl->d_cu.alloc((size_t)(B + 1) * 4);
   if (pl->d_row_pos.bytes < (size_t)T * 4 || !pl->d_row_pos.p) pl->d_row_pos.alloc(std::max<int64_t>(T, 1) * 4);
   if (pl->d_row_seq.bytes < (size_t)T * 4 || !pl->d_row_seq.p) pl->d_row_seq.alloc(std::max<int64_t>(T, 1) * 4);
-  if (pl->d_tiles.bytes < tiles.size() * sizeof(int2) || !pl->d_tiles.p) pl->d_tiles.alloc(tiles.size() * sizeof(int2));
-  if (pl->d_tiles_first.bytes < tiles_first.size() * sizeof(int2) || !pl->d_tiles_first.p)
-    pl->d_tiles_first.alloc(tiles_first.size() * sizeof(int2));
+  if (pl->d_tiles.bytes < tiles.size() * sizeof(int4) || !pl->d_tiles.p) pl->d_tiles.alloc(tiles.size() * sizeof(int4));
+  if (pl->d_tiles_first.bytes < tiles_first.size() * sizeof(int4) || !pl->d_tiles_first.p)
+    pl->d_tiles_first.alloc(tiles_first.size() * sizeof(int4));
   KH_CHECK(hipStreamSynchronize(pl->stream));  // staging may still feed an earlier copy
   // eight blocks at most (cu, row_pos, row_seq, tiles, first tiles, type ids, ids, markers), each
   // 16-byte aligned
   const size_t T1 = (size_t)std::max<int64_t>(T, 1);
-  const size_t meta = (size_t)(B + 1) * 4 + 4 * T1 * 4 + (tiles.size() + tiles_first.size()) * sizeof(int2) +
+  const size_t meta = (size_t)(B + 1) * 4 + 4 * T1 * 4 + (tiles.size() + tiles_first.size()) * sizeof(int4) +
                       pl->markers_host.size() * 4 + 8 * 16;
   pl->pin_meta.ensure(meta);
   char *mp = (char *)pl->pin_meta.p;
@@ -1037,8 +1037,8 @@ static void pack(kh_plan *pl, int rows, int b_end) {
   put(pl->d_cu, pl->cu.data(), (size_t)(B + 1) * 4);
   put(pl->d_row_pos, row_pos.data(), (size_t)std::max<int64_t>(T, 1) * 4);
   put(pl->d_row_seq, row_seq.data(), (size_t)std::max<int64_t>(T, 1) * 4);
-  put(pl->d_tiles, tiles.data(), tiles.size() * sizeof(int2));
-  put(pl->d_tiles_first, tiles_first.data(), tiles_first.size() * sizeof(int2));
+  put(pl->d_tiles, tiles.data(), tiles.size() * sizeof(int4));
+  put(pl->d_tiles_first, tiles_first.data(), tiles_first.size() * sizeof(int4));
   // packed type ids
   if (!pl->in_tt.empty()) {
     // type rows the embedding reads must exist (an out-of-range id would read past the table)

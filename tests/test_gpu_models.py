@@ -119,11 +119,15 @@ def test_device_ids_without_position_tables(key):
         assert np.abs(rows - ids).max() <= 2e-2
 
 
-def test_fused_product_steps_match_separate_ops(monkeypatch):
+@pytest.mark.parametrize("tile", [None, "9", "12", "14"], ids=["picked", "192x256", "128x384", "256x256"])
+def test_fused_product_steps_match_separate_ops(monkeypatch, tile):
     """ModernBERT: GEMM + GeGLU, GEMM + RoPE and GEMM + residual add run fused in the product's
     epilogue; with fusion off (KH_NO_FUSION) the separate kernels run. Both apply the same f32
-    formulas to the same f16 products, so the results are identical."""
+    formulas to the same f16 products, so the results are identical, whatever tile the products
+    run in (KH_GEMM_TILE forces one for every product)."""
     case, ref = case_and_oracle("c4")
+    if tile:
+        monkeypatch.setenv("KH_GEMM_TILE", tile)
     fused = hip_outputs(case, f16=True)
     monkeypatch.setenv("KH_NO_FUSION", "1")
     separate = hip_outputs(case, f16=True)

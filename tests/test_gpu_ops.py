@@ -99,7 +99,7 @@ def test_matmul_against_f64(f16, N, K, lens):
         assert np.all(out[~valid] == 0), "padding rows must read back as zero"
 
 
-@pytest.mark.parametrize("tile", list(range(14)))
+@pytest.mark.parametrize("tile", list(range(15)))
 def test_matmul_every_tile_configuration(tile, monkeypatch):
     """Each GEMM tile configuration (forced through KH_GEMM_TILE) on a ragged f16 batch whose rows
     end inside a tile, against f64."""
