@@ -7,9 +7,11 @@
  * only; every entry point returns KH_OK (0) or an error code, and kh_last_error() gives the
  * message of the calling thread's last failure.
  *
- * Execution model: a plan's rows are stored packed (the valid rows of each sequence back to back,
- * cu_seqlens), derived from the prefix mask at the first run after an upload. Only valid rows are
- * computed; per-row outputs (token heads) are scattered back to the plan's b * L + i layout on read.
+ * Execution model: a plan's rows are stored packed (the rows of each sequence up to its last
+ * nonzero mask value, back to back, cu_seqlens), derived from the mask at the first run after an
+ * upload. Only those rows are computed; per-row outputs (token heads) are scattered back to the
+ * plan's b * L + i layout on read. A mask that is not a 0/1 prefix is executed as the reference's
+ * executor does (keys and queries count above 0.5, the mean pool and MASKMUL weigh by the value).
  * One HIP stream per plan; a context is single-threaded by contract (one call in flight per plan,
  * as src/encoder.ts:5-8 and 265-269 guarantee on the reference side).
  */
@@ -186,8 +188,8 @@ int kh_plan_info_get(const kh_plan *plan, kh_plan_info *out);
 
 /* PlanRunner.upload (src/plan/executor.ts:365-393): word rows [L * B, E] in the plan's storage
  * dtype, the f32 mask [L * B] and, for plans with a typeIds input, u32 type ids [L * B] (position
- * row in the high 16 bits for POSIDS). Copied before return; the mask must be a prefix mask of
- * 0/1 per sequence (as every reference engine fills it, src/wasm/plan.ts:13-14). */
+ * row in the high 16 bits for POSIDS). Copied before return. Any mask values: rows up to a
+ * sequence's last nonzero value are computed (src/wasm/plan.ts:556-582, 474-495). */
 int kh_upload(kh_plan *plan, const void *emb, size_t emb_bytes, const float *mask, size_t mask_count,
               const uint32_t *type_ids, size_t type_count);
 

@@ -89,10 +89,12 @@ __device__ __forceinline__ uint4 load_chunk(const T *row, int d, int Dr) {
 }
 
 // Four wavefronts per SIMD on the standard path (short sequences are latency-bound), two on the
-// relative path (half of each with PAD, whose element-wise loads hold more registers). WIN: a
-// sliding window (a.window > 0) bounds the keys of each query.
-template <typename T, int D, bool REL, bool WIN, bool PAD>
-__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(PAD ? (REL ? 1 : 2) : (REL ? 2 : 4), 8)))
+// relative path (half of each with PAD, whose element-wise loads hold more registers, or KM). WIN:
+// a sliding window (a.window > 0) bounds the keys of each query. KM: masks other than 0/1 prefixes
+// (p.row_w), a separate instantiation so the usual kernels keep their registers.
+template <typename T, int D, bool REL, bool WIN, bool PAD, bool KM>
+__global__ void __launch_bounds__(128)
+__attribute__((amdgpu_waves_per_eu((PAD || KM) ? (REL ? 1 : 2) : (REL ? 2 : 4), 8)))
 attn_kernel(AttnArgs a, Packing p) {
   typedef AttnMfma<T> MF;
   const int Dr = PAD ? a.D : D;           // the rows' head dimension
@@ -111,6 +113,7 @@ attn_kernel(AttnArgs a, Packing p) {
   constexpr int RP = 68;  // relative scratch pitch (floats)
   __shared__ __attribute__((aligned(16))) float sRel[REL ? 2 * 32 * RP : 1];  // [wave][32][RP]
   extern __shared__ short sBucket[];  // [2 lmax - 1] (dynamic: the relative path only)
+  __shared__ float sKw[KM ? KT : 1];   // the key tile's mask values (masks other than 0/1 prefixes)
 
   // items (head, query tile), tiles fastest: the query tiles of one sequence and head run
   // together on one XCD and find its K and V rows in that XCD's L2
@@ -129,6 +132,10 @@ attn_kernel(AttnArgs a, Packing p) {
   const int qi = q0 + w * 32 + (lane & 31);      // this lane's query (column)
   const bool qvalid = qi < n;
   const int qc = qvalid ? qi : n - 1;
+  // masks other than 0/1 prefixes (p.row_w): keys count where their mask value exceeds 0.5, and a
+  // query row whose value does not writes zeros (src/wasm/plan.ts:573-582)
+  const float *kw = KM ? p.row_w : nullptr;
+  const bool qkeep = !KM || kw[base + qc] > 0.5f;
 
   // Q fragments: B operand of S^T = K Q^T (column = query, k = d)
   typename MF::frag qf[QS];
@@ -203,6 +210,8 @@ attn_kernel(AttnArgs a, Packing p) {
         *reinterpret_cast<vec4_t *>(&sVt[(dc + e) * LDV + kr]) = col;
       }
     }
+    if constexpr (KM)
+      for (int i = t; i < KT; i += 128) sKw[i] = kb + i < khi ? kw[base + kb + i] : 0.f;
     __syncthreads();
 
     // S^T sub-tiles: 32 keys x 32 queries each
@@ -288,6 +297,13 @@ attn_kernel(AttnArgs a, Packing p) {
         term(std::true_type{});
       }
       const int k0 = kb + kt * 32;
+      // bit r: the key of register r has a mask value above 0.5 (all set for 0/1 prefix masks)
+      [[maybe_unused]] uint32_t kbits = 0xffffu;
+      if constexpr (KM) {
+        kbits = 0;
+#pragma unroll
+        for (int r = 0; r < 16; r++) kbits |= (sKw[kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3)] > 0.5f ? 1u : 0u) << r;
+      }
       auto scores = [&](auto masked_t) {
         constexpr bool MASKED = decltype(masked_t)::value;
         [[maybe_unused]] const int lim = khi - k0;  // keys jl < lim exist
@@ -298,6 +314,7 @@ attn_kernel(AttnArgs a, Packing p) {
           float v = sc[kt][r];
           if constexpr (MASKED) {
             bool ok = jl < lim;
+            if constexpr (KM) ok = ok && ((kbits >> r) & 1u);
             if constexpr (WIN) ok = ok && jl >= wlo && jl <= whi;
             v = ok ? v : -INFINITY;
           }
@@ -305,7 +322,7 @@ attn_kernel(AttnArgs a, Packing p) {
           tmax = fmaxf(tmax, v);
         }
       };
-      if (WIN || k0 + 32 > khi) scores(std::true_type{});
+      if (WIN || KM || k0 + 32 > khi) scores(std::true_type{});
       else scores(std::false_type{});
     }
     tmax = fmaxf(tmax, xor32(tmax));
@@ -371,7 +388,7 @@ attn_kernel(AttnArgs a, Packing p) {
   }
 
   const float l_tot = l_run + xor32(l_run);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const float inv = l_tot > 0.f && qkeep ? 1.f / l_tot : 0.f;
   // The output tile leaves through LDS (the K tile's space, free after the key loop's last
   // barrier): a lane holds 4-value pieces of one query row, scattered over 32 rows per store;
   // staged, every row goes out as whole 16-byte chunks.
@@ -414,10 +431,15 @@ void launch_w(const AttnArgs &a, const Packing &p, hipStream_t s) {
   // the relative path's bucket table: 2 lmax - 1 16-bit entries of dynamic LDS
   const unsigned dyn = REL ? (unsigned)((2 * a.lmax - 1) * sizeof(short) + 3) / 4 * 4 : 0;
   // head dimensions 32 and 64 as they are; others padded to the next of the two (up to 64)
-  if (a.D == 64) launch((attn_kernel<T, 64, REL, WIN, false>), grid, dim3(128), dyn, s, a, p);
-  else if (a.D == 32) launch((attn_kernel<T, 32, REL, WIN, false>), grid, dim3(128), dyn, s, a, p);
-  else if (a.D < 32) launch((attn_kernel<T, 32, REL, WIN, true>), grid, dim3(128), dyn, s, a, p);
-  else launch((attn_kernel<T, 64, REL, WIN, true>), grid, dim3(128), dyn, s, a, p);
+  auto go = [&](auto km_t) {
+    constexpr bool KM = decltype(km_t)::value;
+    if (a.D == 64) launch((attn_kernel<T, 64, REL, WIN, false, KM>), grid, dim3(128), dyn, s, a, p);
+    else if (a.D == 32) launch((attn_kernel<T, 32, REL, WIN, false, KM>), grid, dim3(128), dyn, s, a, p);
+    else if (a.D < 32) launch((attn_kernel<T, 32, REL, WIN, true, KM>), grid, dim3(128), dyn, s, a, p);
+    else launch((attn_kernel<T, 64, REL, WIN, true, KM>), grid, dim3(128), dyn, s, a, p);
+  };
+  if (p.row_w) go(std::true_type{});
+  else go(std::false_type{});
 }
 
 template <typename T, bool REL>

@@ -65,12 +65,16 @@ bool gemm_uses_mfma(bool f16, const GemmArgs &g);
 bool gemm_epi_ok(bool f16, const GemmArgs &g);
 
 // Packed-row description of one run: cu[b] .. cu[b+1] are the rows of sequence b.
+// With masks that are not 0/1 prefixes, a sequence's packed rows run to its last nonzero mask
+// value and row_w [T] holds each row's mask value: keys and queries count where it exceeds 0.5,
+// pooling and the mask-multiplied embeddings weigh by it. row_w is null for 0/1 prefix masks.
 struct Packing {
   const int32_t *cu;       // [B + 1]
   const int32_t *row_pos;  // [T] position of the row inside its sequence
   const int32_t *row_seq;  // [T] sequence of the row
   int32_t B;
   int64_t T;
+  const float *row_w = nullptr;  // [T] mask values, or null (every packed row 1)
 };
 
 
@@ -97,6 +101,7 @@ struct EmbLnArgs {
   void *out = nullptr;
   int N = 0, offset = 0, maxpos = 1, posids = 0;
   float eps = 0.f;
+  const float *row_scale = nullptr;  // [T] multiplies each output row (MASKMUL), or null
 };
 void embln(bool f16, const EmbLnArgs &a, const Packing &p, hipStream_t s, const PrefetchArgs &pf = PrefetchArgs());
 
@@ -107,9 +112,10 @@ void mask_logits(bool f16, const void *raw, const uint32_t *packed, float *logit
 
 // LN over rows: MODE 2 adds b first. rows = T (packed) or B (sequence rows). With ids, row r is
 // row ids[r] of a (the device word table), with the arithmetic of the same LN over gathered rows.
+// row_scale [rows], when given, multiplies each output row (MODE 1, the mask-multiplied embedding).
 void layernorm(bool f16, const void *a, const void *b, const void *gamma, const void *beta, void *out,
                int64_t rows, int N, float eps, hipStream_t s, const int32_t *ids = nullptr,
-               const PrefetchArgs &pf = PrefetchArgs());
+               const PrefetchArgs &pf = PrefetchArgs(), const float *row_scale = nullptr);
 
 // dst += src (MODE 0) or dst[r] += src[seq(r)] (MODE 1), rounded to storage.
 void add(bool f16, void *dst, const void *src, int64_t rows, int N, int mode, const Packing &p,

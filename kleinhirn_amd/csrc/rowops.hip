@@ -39,7 +39,7 @@ __device__ __forceinline__ void prefetch_share(const PrefetchArgs &pf) {
 // Per lane: PER groups of VEC contiguous elements; group g = k * 64 + lane.
 template <typename T, int VEC, int PER>
 __device__ __forceinline__ void ln_finish(float (&v)[PER][VEC], int N, const T *gamma, const T *beta,
-                                          float eps, T *out, int lane) {
+                                          float eps, T *out, int lane, const float *scale) {
   float s = 0.f;
 #pragma unroll
   for (int k = 0; k < PER; k++) {
@@ -69,6 +69,11 @@ __device__ __forceinline__ void ln_finish(float (&v)[PER][VEC], int N, const T *
     if (beta) VecIO<T, VEC>::load(beta + e0, b);
 #pragma unroll
     for (int i = 0; i < VEC; i++) y[i] = (v[k][i] - mean) * inv * g[i] + (beta ? b[i] : 0.f);
+    if (scale) {
+      const float sc = *scale;
+#pragma unroll
+      for (int i = 0; i < VEC; i++) y[i] *= sc;
+    }
     VecIO<T, VEC>::store(out + e0, y);
   }
 }
@@ -77,7 +82,8 @@ template <typename T, int VEC, int PER>
 __global__ void __launch_bounds__(256) layernorm_kernel(const T *__restrict__ a, const T *__restrict__ b,
                                                         const T *__restrict__ gamma, const T *__restrict__ beta,
                                                         T *__restrict__ out, int64_t rows, int N, float eps,
-                                                        const int32_t *__restrict__ ids, PrefetchArgs pf) {
+                                                        const int32_t *__restrict__ ids, PrefetchArgs pf,
+                                                        const float *__restrict__ row_scale) {
   int lane = threadIdx.x & 63;
   int64_t r = (int64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
   if (r >= rows) {
@@ -103,7 +109,7 @@ __global__ void __launch_bounds__(256) layernorm_kernel(const T *__restrict__ a,
       for (int i = 0; i < VEC; i++) v[k][i] = 0.f;
     }
   }
-  ln_finish<T, VEC, PER>(v, N, gamma, beta, eps, out + r * N, lane);
+  ln_finish<T, VEC, PER>(v, N, gamma, beta, eps, out + r * N, lane, row_scale ? row_scale + r : nullptr);
   prefetch_share(pf);
 }
 
@@ -116,7 +122,8 @@ __global__ void __launch_bounds__(256) layernorm_rows_kernel(const T *__restrict
                                                              const T *__restrict__ gamma,
                                                              const T *__restrict__ beta, T *__restrict__ out,
                                                              int64_t rows, int N, float eps,
-                                                             const int32_t *__restrict__ ids, PrefetchArgs pf) {
+                                                             const int32_t *__restrict__ ids, PrefetchArgs pf,
+                                                             const float *__restrict__ row_scale) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int RPW = WAVE / LPR;  // rows per wavefront
   const int lane = threadIdx.x & 63, l = lane % LPR;
@@ -167,6 +174,11 @@ __global__ void __launch_bounds__(256) layernorm_rows_kernel(const T *__restrict
     if (beta) VecIO<T, VEC>::load(beta + e0, bt);
 #pragma unroll
     for (int i = 0; i < VEC; i++) y[i] = (v[k][i] - mean) * inv * gm[i] + (beta ? bt[i] : 0.f);
+    if (row_scale) {
+      const float sc = row_scale[r];
+#pragma unroll
+      for (int i = 0; i < VEC; i++) y[i] *= sc;
+    }
     VecIO<T, VEC>::store(out + r * N + e0, y);
   }
   prefetch_share(pf);
@@ -206,7 +218,8 @@ __global__ void __launch_bounds__(256) embln_kernel(EmbLnArgs a, Packing p, Pref
       for (int i = 0; i < VEC; i++) v[k][i] = 0.f;
     }
   }
-  ln_finish<T, VEC, PER>(v, N, (const T *)a.gamma, (const T *)a.beta, a.eps, (T *)a.out + r * N, lane);
+  ln_finish<T, VEC, PER>(v, N, (const T *)a.gamma, (const T *)a.beta, a.eps, (T *)a.out + r * N, lane,
+                         a.row_scale ? a.row_scale + r : nullptr);
   prefetch_share(pf);
 }
 
@@ -236,7 +249,8 @@ bool dispatch_per(int N, F &&f) {
 
 template <typename T>
 void layernorm_t(const void *a, const void *b, const void *gamma, const void *beta, void *out, int64_t rows,
-                 int N, float eps, const int32_t *ids, const PrefetchArgs &pf, hipStream_t s) {
+                 int N, float eps, const int32_t *ids, const PrefetchArgs &pf, const float *row_scale,
+                 hipStream_t s) {
   // rows of 3 x 2^j 16-byte chunks (384- and 768-wide f16, 384-wide f32): groups of 2^j lanes
   constexpr int VEC16 = 16 / sizeof(T);
   if (N % (3 * VEC16) == 0) {
@@ -245,7 +259,8 @@ void layernorm_t(const void *a, const void *b, const void *gamma, const void *be
       constexpr int LPR = decltype(lpr_t)::value;
       const int64_t per_block = (int64_t)ROWS_PER_BLOCK * (WAVE / LPR);
       launch((layernorm_rows_kernel<T, LPR, 3>), dim3((unsigned)((rows + per_block - 1) / per_block)), dim3(256),
-             0, s, (const T *)a, (const T *)b, (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps, ids, pf);
+             0, s, (const T *)a, (const T *)b, (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps, ids, pf,
+             row_scale);
     };
     switch (lpr) {
       case 8: go_rows(std::integral_constant<int, 8>()); return;
@@ -261,7 +276,7 @@ void layernorm_t(const void *a, const void *b, const void *gamma, const void *be
     dispatch_per<T, VEC>(N, [&](auto per) {
       constexpr int PER = decltype(per)::value;
       launch((layernorm_kernel<T, VEC, PER>), grid, dim3(256), 0, s, (const T *)a, (const T *)b,
-                         (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps, ids, pf);
+                         (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps, ids, pf, row_scale);
     });
   };
   // 16-byte loads where the width allows
@@ -356,12 +371,32 @@ __global__ void __launch_bounds__(256) rope_kernel(T *__restrict__ qkv, const fl
 // valid rows of a packed sequence are all its rows.
 template <typename T>
 __global__ void __launch_bounds__(64) pool_kernel(const T *__restrict__ x, T *__restrict__ out, int N, int mode,
-                                                  const int32_t *__restrict__ cu) {
+                                                  const int32_t *__restrict__ cu, const float *__restrict__ w) {
   int b = blockIdx.y;
   int d = blockIdx.x * 64 + threadIdx.x;
   if (d >= N) return;
   int r0 = cu[b], r1 = cu[b + 1];
   float acc = 0.f;
+  if (w) {
+    // masks that are not 0/1 prefixes: the mean weighs each row by its mask value (rows of value 0
+    // skipped), the maximum takes the rows whose value exceeds 0.5 (src/wasm/plan.ts:474-495)
+    float cnt = 0.f;
+    bool found = false;
+    for (int r = r0; r < r1; r++) {
+      const float m = w[r];
+      if (mode == 0) {
+        if (m == 0.f) continue;
+        acc += m * (float)x[(int64_t)r * N + d];
+        cnt += m;
+      } else if (m > 0.5f) {
+        const float v = (float)x[(int64_t)r * N + d];
+        acc = found ? fmaxf(acc, v) : v;
+        found = true;
+      }
+    }
+    out[(int64_t)b * N + d] = (T)(mode == 0 ? acc / fmaxf(cnt, 1e-9f) : acc);
+    return;
+  }
   if (mode == 0) {
     // rows added in order; 8 loads in flight ahead of the chain
     float cnt = 0.f;
@@ -447,10 +482,11 @@ void first_rows(bool f16, const void *src, void *dst, int D, bool from_packed, c
 }
 
 void layernorm(bool f16, const void *a, const void *b, const void *gamma, const void *beta, void *out,
-               int64_t rows, int N, float eps, hipStream_t s, const int32_t *ids, const PrefetchArgs &pf) {
+               int64_t rows, int N, float eps, hipStream_t s, const int32_t *ids, const PrefetchArgs &pf,
+               const float *row_scale) {
   if (rows <= 0) return;
-  if (f16) layernorm_t<half_t>(a, b, gamma, beta, out, rows, N, eps, ids, pf, s);
-  else layernorm_t<float>(a, b, gamma, beta, out, rows, N, eps, ids, pf, s);
+  if (f16) layernorm_t<half_t>(a, b, gamma, beta, out, rows, N, eps, ids, pf, row_scale, s);
+  else layernorm_t<float>(a, b, gamma, beta, out, rows, N, eps, ids, pf, row_scale, s);
 }
 
 void embln(bool f16, const EmbLnArgs &a, const Packing &p, hipStream_t s, const PrefetchArgs &pf) {
@@ -514,9 +550,9 @@ void pool(bool f16, const void *x, void *out, int N, int mode, const Packing &p,
   dim3 grid((unsigned)((N + 63) / 64), (unsigned)p.B);
   if (f16)
     launch((pool_kernel<half_t>), grid, dim3(64), 0, s, (const half_t *)x, (half_t *)out, N, mode,
-                       p.cu);
+                       p.cu, p.row_w);
   else
-    launch((pool_kernel<float>), grid, dim3(64), 0, s, (const float *)x, (float *)out, N, mode, p.cu);
+    launch((pool_kernel<float>), grid, dim3(64), 0, s, (const float *)x, (float *)out, N, mode, p.cu, p.row_w);
 }
 
 void gather_rows(bool f16, const void *x, const uint32_t *markers, void *states, int K, int D, const Packing &p,

@@ -8,7 +8,7 @@
 // no step reads after the fusion (scores, c2p, p2c, kinfo, mask) get no device memory.
 //
 // Per call the host hands padded RunInput arrays (src/plan/executor.ts:25-32); the first run after
-// an upload derives cu_seqlens from the prefix mask, packs the valid rows into pinned memory and
+// an upload derives cu_seqlens from the mask, packs the valid rows into pinned memory and
 // copies only those to the device.
 #include <hip/hip_runtime.h>
 
@@ -143,6 +143,7 @@ struct Step {
   bool rel = false;
   std::string markers_id;  // gather: the init buffer holding the markers
   int epi = 0;             // S_GEMM: fused step (EPI_*); in[4] holds a RoPE table
+  int maskmul = 0;         // S_EMBLN: the output rows times the mask (MASKMUL)
   bool first_tiles = false;  // S_ATTN: only the first query tile of each sequence
 };
 
@@ -240,6 +241,9 @@ struct kh_plan {
   int64_t rows_first = 0;  // query rows of the first tiles
   HostPinned pin_emb, pin_meta;
   DevMem d_cu, d_row_pos, d_row_seq, d_tiles, d_tiles_first, d_tt, d_ids;
+  // masks other than 0/1 prefixes: each packed row's mask value (Packing::row_w)
+  bool masked = false;
+  DevMem d_row_w;
 
   // relative attention
   std::vector<int32_t> bucket_host;
@@ -261,7 +265,17 @@ static Packing packing_of(kh_plan *pl) {
   p.row_seq = (const int32_t *)pl->d_row_seq.p;
   p.B = pl->B;
   p.T = pl->T;
+  p.row_w = pl->masked ? (const float *)pl->d_row_w.p : nullptr;
   return p;
+}
+
+// The rows of a sequence the forward computes: up to its last nonzero mask value. For a 0/1
+// prefix mask these are its valid rows; any other mask keeps its holes and fractional values as
+// rows whose mask value the kernels read (Packing::row_w), as the reference's executor does.
+static int seq_extent(const float *m, int L) {
+  int e = L;
+  while (e > 0 && m[e - 1] == 0.f) e--;
+  return e;
 }
 
 // ---- plan parsing and lowering -------------------------------------------------------------
@@ -399,6 +413,7 @@ static std::vector<Step> lower(const Parsed &pp, bool f16, int L, std::vector<st
         s.maxpos = cint(op, "MAXPOS");
         s.posids = cint(op, "POSIDS");
         s.eps = (float)cnum(op, "EPS");
+        s.maskmul = op.at("constants").has("MASKMUL") ? cint(op, "MASKMUL") : 0;
         if (cint(op, "L") != L) fail(KH_EINVAL, "embln L differs from the plan length");
       } else if (kn == "add") {
         s.kind = S_ADD;
@@ -826,14 +841,15 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook, const 
         // table, so the result equals the LN of the uploaded rows bit for bit
         begin("layernorm", 8.0 * pl->T * s.N, 2.0 * es * pl->T * s.N + 4.0 * pl->T);
         layernorm(f16, pl->ctx->words->p, nullptr, bufp(pl, s.in[2]), bufp(pl, s.in[3]), bufp(pl, s.in[5]), pl->T,
-                  s.N, s.eps, st, (const int32_t *)pl->d_ids.p, pf);
+                  s.N, s.eps, st, (const int32_t *)pl->d_ids.p, pf, s.mode == 1 ? pk.row_w : nullptr);
         end();
         break;
       }
       const void *b = s.mode == 2 ? bufp(pl, s.in[1]) : nullptr;
       begin("layernorm", 8.0 * rows * s.N, (double)es * ((s.mode == 2 ? 3.0 : 2.0) * rows * s.N + 2.0 * s.N));
+      // MODE 1 multiplies by the mask: 1 on every packed row of a 0/1 prefix mask, else row_w
       layernorm(f16, bufp(pl, s.in[0]), b, bufp(pl, s.in[2]), bufp(pl, s.in[3]), bufp(pl, s.in[5]), rows, s.N, s.eps,
-                st, nullptr, pf);
+                st, nullptr, pf, s.mode == 1 && !s.seq_rows ? pk.row_w : nullptr);
       end();
       break;
     }
@@ -853,6 +869,7 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook, const 
       a.maxpos = s.maxpos;
       a.posids = s.posids;
       a.eps = s.eps;
+      a.row_scale = s.maskmul ? pk.row_w : nullptr;
       const int tables = 1 + (a.pos ? 1 : 0) + (a.typ ? 1 : 0);
       begin("embln", 9.0 * pl->T * s.N, (double)es * (tables + 1.0) * pl->T * s.N + 4.0 * pl->T);
       embln(f16, a, pk, st, pf);
@@ -940,22 +957,14 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook, const 
 static void pack(kh_plan *pl, int rows, int b_end) {
   const int L = pl->L, B = pl->B;
   std::vector<int32_t> n(B);
+  bool masked = false;
   for (int b = 0; b < B; b++) {
     const float *m = pl->mask_host.data() + (size_t)b * L;
-    int len = 0;
-    while (len < L && m[len] > 0.5f) len++;
-    for (int i = 0; i < L; i++) {
-      const float v = m[i];
-      if (i < len && v != 1.0f)
-        fail(KH_EINVAL, "mask value " + std::to_string(v) + " at sequence " + std::to_string(b) + " row " +
-                            std::to_string(i) + ": the HIP runner takes 0/1 prefix masks");
-      if (i >= len && v > 0.5f)
-        fail(KH_EINVAL, "mask of sequence " + std::to_string(b) + " has a hole before row " + std::to_string(i) +
-                            ": the HIP runner takes prefix masks");
-    }
+    const int len = seq_extent(m, L);
     int cap = b < b_end ? rows - b * L : 0;
     cap = cap < 0 ? 0 : (cap > L ? L : cap);
     n[b] = len < cap ? len : cap;
+    for (int i = 0; i < n[b] && !masked; i++) masked = m[i] != 1.0f;
   }
   pl->cu.assign(B + 1, 0);
   for (int b = 0; b < B; b++) pl->cu[b + 1] = pl->cu[b] + n[b];
@@ -1023,8 +1032,8 @@ static void pack(kh_plan *pl, int rows, int b_end) {
   // eight blocks at most (cu, row_pos, row_seq, tiles, first tiles, type ids, ids, markers), each
   // 16-byte aligned
   const size_t T1 = (size_t)std::max<int64_t>(T, 1);
-  const size_t meta = (size_t)(B + 1) * 4 + 4 * T1 * 4 + (tiles.size() + tiles_first.size()) * sizeof(int4) +
-                      pl->markers_host.size() * 4 + 8 * 16;
+  const size_t meta = (size_t)(B + 1) * 4 + 5 * T1 * 4 + (tiles.size() + tiles_first.size()) * sizeof(int4) +
+                      pl->markers_host.size() * 4 + 9 * 16;
   pl->pin_meta.ensure(meta);
   char *mp = (char *)pl->pin_meta.p;
   char *const mend = mp + meta;
@@ -1039,6 +1048,14 @@ static void pack(kh_plan *pl, int rows, int b_end) {
   put(pl->d_row_seq, row_seq.data(), (size_t)std::max<int64_t>(T, 1) * 4);
   put(pl->d_tiles, tiles.data(), tiles.size() * sizeof(int4));
   put(pl->d_tiles_first, tiles_first.data(), tiles_first.size() * sizeof(int4));
+  pl->masked = masked;
+  if (masked) {
+    std::vector<float> w(T1, 0.f);
+    for (int b = 0; b < B; b++)
+      for (int i = 0; i < n[b]; i++) w[pl->cu[b] + i] = pl->mask_host[(size_t)b * L + i];
+    if (pl->d_row_w.bytes < T1 * 4 || !pl->d_row_w.p) pl->d_row_w.alloc(T1 * 4);
+    put(pl->d_row_w, w.data(), T1 * 4);
+  }
   // packed type ids
   if (!pl->in_tt.empty()) {
     // type rows the embedding reads must exist (an out-of-range id would read past the table)
@@ -1224,10 +1241,7 @@ static int choose_split(const kh_plan *pl, int rows) {
   if (!per_seq && !per_tok) return 0;
   std::vector<int64_t> pre(pl->B + 1, 0);
   for (int b = 0; b < pl->B; b++) {
-    const float *m = pl->mask_host.data() + (size_t)b * pl->L;
-    int len = 0;
-    while (len < pl->L && m[len] > 0.5f) len++;
-    pre[b + 1] = pre[b] + len;
+    pre[b + 1] = pre[b] + seq_extent(pl->mask_host.data() + (size_t)b * pl->L, pl->L);
   }
   const int64_t T = pre[pl->B];
   if (T < env_int("KH_SPLIT_MIN", 2048) || T >= env_int("KH_SPLIT_T", 400000)) return 0;
@@ -1310,9 +1324,7 @@ static void stage_twin(kh_plan *pl, int split) {
     if (t->emb_host.size() != M * row) t->emb_host.resize(M * row);
     t->emb_valid = t->emb_host.size();
     for (int b = split; b < pl->B; b++) {
-      const float *m = pl->mask_host.data() + (size_t)b * L;
-      size_t len = 0;
-      while (len < L && m[len] > 0.5f) len++;
+      const size_t len = (size_t)seq_extent(pl->mask_host.data() + (size_t)b * L, (int)L);
       const size_t src = (size_t)b * L * row, dst = (size_t)(b - split) * L * row;
       if (src + len * row > pl->emb_valid) fail(KH_EINVAL, "word rows shorter than the mask's valid rows");
       if (len) memcpy(t->emb_host.data() + dst, pl->emb_host.data() + src, len * row);
@@ -1948,9 +1960,7 @@ int kh_upload(kh_plan *plan, const void *emb, size_t emb_bytes, const float *mas
   if (plan->emb_host.size() != M * row) plan->emb_host.assign(M * row, 0);
   plan->emb_valid = emb_bytes;
   for (int b = 0; b < plan->B; b++) {
-    const float *m = plan->mask_host.data() + (size_t)b * L;
-    size_t len = 0;
-    while (len < L && m[len] > 0.5f) len++;
+    const size_t len = (size_t)seq_extent(plan->mask_host.data() + (size_t)b * L, (int)L);
     const size_t from = (size_t)b * L * row;
     const size_t n = from >= emb_bytes ? 0 : std::min(len * row, emb_bytes - from);
     if (n) memcpy(plan->emb_host.data() + from, (const uint8_t *)emb + from, n);

@@ -1,8 +1,8 @@
 // HIP backend: the Backend / PlanRunner seam (src/backend.ts:14-46 of kleinhirn) on one MI355X
 // through libkh_hip.so (include/kh_hip.h) and its Node-API binding kh_addon.node. Drop-in beside
 // src/webgpu-backend.ts and src/wasm-backend.ts: the plans of src/plan/build.ts run unchanged; the
-// library stores each plan's rows packed (cu_seqlens from the prefix mask) and computes only the
-// valid rows on hand-written gfx950 kernels.
+// library stores each plan's rows packed (cu_seqlens from the mask) and computes only the valid
+// rows on hand-written gfx950 kernels.
 //
 // Node only (a native addon). Integration in the host repository:
 //   * widen Backend.kind in src/backend.ts to 'webgpu' | 'wasm' | 'hip';

@@ -399,3 +399,93 @@ def test_add_geglu_rope_pool_gather(f16):
             seq = x64[b * L:b * L + n]
             want = seq.mean(0) if kind == "mean" else seq.max(0) if kind == "max" else seq[0]
             close(out[b], want, tol, f"pool {kind}")
+
+
+def attention_ref_masked(qkv, mask, L, H, D, scale, window=0, rel=None):
+    """f64 attention with the reference's general masking (src/wasm/plan.ts:573-582, 652-661):
+    keys count where the mask exceeds 0.5, a query row whose mask does not is zero, every other
+    query attends over the counted keys (and its window)."""
+    hd = H * D
+    B = len(mask) // L
+    out = np.zeros((L * B, hd))
+    q64 = qkv.astype(np.float64)
+    for b in range(B):
+        m = mask[b * L:(b + 1) * L]
+        keys = np.nonzero(m > 0.5)[0]
+        for i in np.nonzero(m > 0.5)[0]:
+            row = q64[b * L + i]
+            for h in range(H):
+                q = row[h * D:(h + 1) * D]
+                ks = keys if not window else keys[np.abs(keys - i) <= window]
+                k = q64[b * L + ks][:, (H + h) * D:(H + h + 1) * D]
+                v = q64[b * L + ks][:, (2 * H + h) * D:(2 * H + h + 1) * D]
+                s = k @ q
+                if rel is not None:
+                    idx, pk, pq = rel
+                    p = idx[i * L + ks]
+                    s = (s + pk[p][:, h * D:(h + 1) * D] @ q + np.einsum("jd,jd->j", k, pq[p][:, h * D:(h + 1) * D])) / scale
+                else:
+                    s = s * scale
+                e = np.exp(s - s.max())
+                out[b * L + i, h * D:(h + 1) * D] = (e / e.sum()) @ v
+    return out
+
+
+def holed_mask(L, lens, seed):
+    """Prefix masks with holes (0 inside), fractional values (0.7 counts as a key, 0.3 does not),
+    a masked first row, and a trailing row of 0.4 past the last key."""
+    rng = np.random.default_rng(seed)
+    m = np.zeros(L * len(lens), dtype=np.float32)
+    for b, n in enumerate(lens):
+        v = np.ones(n, dtype=np.float32)
+        if n > 8:
+            for i in rng.choice(np.arange(1, n - 1), size=max(1, n // 8), replace=False):
+                v[i] = rng.choice([0.0, 0.7, 0.3])
+        if b == 1:
+            v[0] = 0.0
+        m[b * L:b * L + n] = v
+        if n < L:
+            m[b * L + n] = 0.4
+    return m
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("kind", ["standard", "window", "relative"])
+def test_attention_with_general_masks(f16, kind):
+    """Masks with holes and fractional values: the kernels' key test and zeroed query rows
+    against the reference's rule in f64."""
+    H, D = 2, 64
+    lens = [150, 70, 9]
+    L = 160
+    B = len(lens)
+    hd = H * D
+    dt = np.float16 if f16 else np.float32
+    qkv = RNG.standard_normal((L * B, 3 * hd)).astype(dt)
+    mask = holed_mask(L, lens, 3)
+    window = 16 if kind == "window" else 0
+    rel = None
+    weights = {}
+    if kind == "relative":
+        span, maxpos = 32, 64
+        pk = RNG.standard_normal((2 * span, hd)).astype(dt)
+        pq = RNG.standard_normal((2 * span, hd)).astype(dt)
+        idx = rel_pos_table(L, span, maxpos)
+        scale = math.sqrt(3 * D)
+        ops = [{"name": "a", "kernel": "attention", "constants": {"L": L, "H": H, "D": D, "SCALE": scale},
+                "bind": ["emb", "w:pk", "w:pq", "relidx", "mask", "ctx"], "dispatch": [H, "rows"]}]
+        extra = {"relidx": idx, "ctx": L * B * hd}
+        weights = {"pk": pk, "pq": pq}
+        rel = (idx, pk.astype(np.float64), pq.astype(np.float64))
+    else:
+        scale = D ** -0.5
+        ops = [{"name": "a", "kernel": "mbflash", "constants": {"L": L, "H": H, "D": D, "SCALE": scale,
+                                                               "WINDOW": window, "ROWS": L * B},
+                "bind": ["emb", "mask", "ctx"], "dispatch": [H, "rows32"]}]
+        extra = {"ctx": L * B * hd}
+    plan = mini_plan(f16, L, B, 3 * hd, ops, extra, "ctx", hd)
+    out = run_plan(plan, weights, qkv, mask, L * B).reshape(L * B, hd)
+    want = attention_ref_masked(qkv, mask, L, H, D, scale, window, rel)
+    keep = mask > 0.5
+    close(out[keep], want[keep], 1e-2 if f16 else 1e-5, f"{kind} attention, general masks")
+    masked_rows = (mask != 0) & ~keep  # computed rows whose mask does not count them: zeros
+    assert np.all(out[masked_rows] == 0)
