@@ -221,8 +221,13 @@ struct kh_plan {
   std::vector<hipEvent_t> ev_pool;
 
   // upload staging (host, padded layout as the caller gave it)
-  std::vector<uint8_t> emb_host;  // padded [L * B, E] layout; only the valid rows are filled
-  size_t emb_valid = 0;           // bytes the caller's array held (rows past it were not given)
+  // The uploaded word rows, packed once at upload into pinned memory: sequence b's first avail[b]
+  // rows (up to its mask extent, and what the caller's array held) at row up_cu[b] of up_rows.
+  // up_rows is this plan's pin_up, or for a twin the primary plan's, at its first moved sequence.
+  HostPinned pin_up, pin_pack;
+  const uint8_t *up_rows = nullptr;
+  std::vector<int64_t> up_cu;
+  std::vector<int32_t> avail;
   std::vector<float> mask_host;
   std::vector<uint32_t> tt_host;
   std::vector<int32_t> ids_host;
@@ -239,7 +244,7 @@ struct kh_plan {
   double attn_pairs_first = 0;  // the same for the first query tile of each sequence
   std::map<int, double> attn_pairs_first_window;
   int64_t rows_first = 0;  // query rows of the first tiles
-  HostPinned pin_emb, pin_meta;
+  HostPinned pin_meta;
   DevMem d_cu, d_row_pos, d_row_seq, d_tiles, d_tiles_first, d_tt, d_ids;
   // masks other than 0/1 prefixes: each packed row's mask value (Packing::row_w)
   bool masked = false;
@@ -1117,16 +1122,24 @@ static void pack(kh_plan *pl, int rows, int b_end) {
   } else {
     const size_t row = (size_t)pl->E * es;
     Buffer &eb = pl->bufs.at(pl->in_emb);
-    pl->pin_emb.ensure(std::max<size_t>((size_t)T * row, 16));
-    char *dst = (char *)pl->pin_emb.p;
-    for (int b = 0; b < B; b++) {
-      const size_t src = (size_t)b * L * row;
-      const size_t nb = (size_t)n[b] * row;
-      if (src + nb > pl->emb_valid) fail(KH_EINVAL, "word rows shorter than the mask's valid rows");
-      memcpy(dst + (size_t)pl->cu[b] * row, pl->emb_host.data() + src, nb);
-    }
     if ((size_t)T * row > eb.mem->bytes) fail(KH_EINVAL, "packed rows exceed the emb buffer");
-    if (T > 0) KH_CHECK(hipMemcpyAsync(eb.mem->p, pl->pin_emb.p, (size_t)T * row, hipMemcpyHostToDevice, pl->stream));
+    // the upload packed each sequence's rows already: when this run takes all of them (the usual
+    // case) they go to the device as they are; a run that takes fewer rows of some sequence (a
+    // smaller row count) copies its rows once more, into pin_pack
+    bool same = true;
+    for (int b = 0; b < B; b++) {
+      if (n[b] > pl->avail[b]) fail(KH_EINVAL, "word rows shorter than the mask's valid rows");
+      same = same && pl->cu[b] == pl->up_cu[b] && n[b] == pl->avail[b];
+    }
+    const uint8_t *src = pl->up_rows;
+    if (!same && T > 0) {
+      pl->pin_pack.ensure((size_t)T * row);
+      for (int b = 0; b < B; b++)
+        if (n[b]) memcpy((char *)pl->pin_pack.p + (size_t)pl->cu[b] * row, pl->up_rows + (size_t)pl->up_cu[b] * row,
+                         (size_t)n[b] * row);
+      src = (const uint8_t *)pl->pin_pack.p;
+    }
+    if (T > 0) KH_CHECK(hipMemcpyAsync(eb.mem->p, src, (size_t)T * row, hipMemcpyHostToDevice, pl->stream));
   }
   pl->dirty = false;
   pl->last_rows = rows;
@@ -1319,15 +1332,15 @@ static void stage_twin(kh_plan *pl, int split) {
     t->ids_host.assign(M, 0);
     memcpy(t->ids_host.data(), pl->ids_host.data() + from, moved * 4);
   } else {
-    // only the valid rows of each moved sequence (pack reads no others): about T / 2 rows
+    // the moved sequences' rows stay where this plan's upload packed them (contiguous from the
+    // split's first row): the twin's copy to the device reads them there
     const size_t row = (size_t)pl->E * (pl->f16 ? 2 : 4);
-    if (t->emb_host.size() != M * row) t->emb_host.resize(M * row);
-    t->emb_valid = t->emb_host.size();
+    t->up_rows = pl->up_rows + (size_t)pl->up_cu[split] * row;
+    t->up_cu.assign(pl->B + 1, pl->up_cu[pl->B] - pl->up_cu[split]);
+    t->avail.assign(pl->B, 0);
     for (int b = split; b < pl->B; b++) {
-      const size_t len = (size_t)seq_extent(pl->mask_host.data() + (size_t)b * L, (int)L);
-      const size_t src = (size_t)b * L * row, dst = (size_t)(b - split) * L * row;
-      if (src + len * row > pl->emb_valid) fail(KH_EINVAL, "word rows shorter than the mask's valid rows");
-      if (len) memcpy(t->emb_host.data() + dst, pl->emb_host.data() + src, len * row);
+      t->up_cu[b - split] = pl->up_cu[b] - pl->up_cu[split];
+      t->avail[b - split] = pl->avail[b];
     }
   }
   t->uploaded = true;
@@ -1361,16 +1374,40 @@ static void launch_forward(kh_plan *pl, int rows, const LaunchHook &hook, bool s
   pl->split = split;
   ensure_rel(pl);
   kh_plan *t = pl->twin;
-  if (split > 0) {
+  if (split > 0 && !hook) {
+    // both halves packed (the second reads the rows this plan's upload packed, in place), then
+    // their launches interleaved step by step, so that both streams have work from the start (a
+    // call that uploads, runs and reads back pays the host's launch time once, not half after half)
     if (t->dirty) pack(t, t->L * t->B, t->B);
     ensure_rel(t);
+    KH_CHECK(hipEventRecord(pl->ev0, pl->stream));
+    // the twin's half starts with this call, not when the twin finished the previous call's half
+    // (ev0 follows everything queued before on the plan's stream, the previous call's end included)
+    KH_CHECK(hipStreamWaitEvent(t->stream, pl->ev0, 0));
+    const std::vector<Step> &s1 = active_steps(pl), &s2 = active_steps(t);
+    const bool pf = env_int("KH_NO_PREFETCH", 0) == 0;
+    auto step = [&](kh_plan *p, const std::vector<Step> &st, size_t i) {
+      const bool ln = (st[i].kind == S_LN || st[i].kind == S_EMBLN) && !st[i].seq_rows;
+      exec_step(p, st[i], hook, pf && ln ? prefetch_for(p, st, i) : PrefetchArgs());
+    };
+    for (size_t i = 0; i < std::max(s1.size(), s2.size()); i++) {
+      if (i < s1.size()) step(pl, s1, i);
+      if (i < s2.size()) step(t, s2, i);
+    }
+    KH_CHECK(hipGetLastError());
+    KH_CHECK(hipEventRecord(pl->ev_twin, t->stream));
+    KH_CHECK(hipStreamWaitEvent(pl->stream, pl->ev_twin, 0));
+    t->ran = true;
+    KH_CHECK(hipEventRecord(pl->ev1, pl->stream));
+    pl->ran = true;
+    return;
   }
   KH_CHECK(hipEventRecord(pl->ev0, pl->stream));
   run_steps(pl, hook);
   if (split > 0) {
+    if (t->dirty) pack(t, t->L * t->B, t->B);
+    ensure_rel(t);
     if (sequential) KH_CHECK(hipStreamSynchronize(pl->stream));  // profiled halves one after the other
-    // the twin's half starts with this call, not when the twin finished the previous call's half
-    // (ev0 follows everything queued before on the plan's stream, the previous call's end included)
     KH_CHECK(hipStreamWaitEvent(t->stream, pl->ev0, 0));
     run_steps(t, hook);
     KH_CHECK(hipEventRecord(pl->ev_twin, t->stream));
@@ -1952,19 +1989,31 @@ int kh_upload(kh_plan *plan, const void *emb, size_t emb_bytes, const float *mas
   if (!emb && emb_bytes) fail(KH_EINVAL, "null word rows");
   if ((int64_t)emb_bytes > eb.bytes)
     fail(KH_EINVAL, "input emb has " + std::to_string(emb_bytes) + " B, the buffer " + std::to_string(eb.bytes));
+  // copies still reading the pinned rows of the previous upload (this plan's, and its twin's,
+  // which reads the same memory) must finish before they are overwritten
+  if (plan->stream) KH_CHECK(hipStreamSynchronize(plan->stream));
+  if (plan->twin && plan->twin->stream) KH_CHECK(hipStreamSynchronize(plan->twin->stream));
   stage_common(plan, mask, mask_count, type_ids, type_count);
-  // only the rows the mask marks valid (each sequence's prefix) are ever packed: copy those, at
-  // their padded positions (a ragged batch of 256 at L = 512 holds ~10 % valid rows)
+  // only the rows a run can read (each sequence's rows up to its last nonzero mask value, a
+  // ragged batch of 256 at L = 512 holds ~10 % of L * B) are copied, once, packed, into pinned
+  // memory: a run that takes them all sends them to the device from there
   const size_t row = (size_t)plan->E * (plan->f16 ? 2 : 4);
-  const size_t L = plan->L, M = L * plan->B;
-  if (plan->emb_host.size() != M * row) plan->emb_host.assign(M * row, 0);
-  plan->emb_valid = emb_bytes;
+  const size_t L = plan->L;
+  plan->up_cu.assign(plan->B + 1, 0);
+  plan->avail.assign(plan->B, 0);
   for (int b = 0; b < plan->B; b++) {
     const size_t len = (size_t)seq_extent(plan->mask_host.data() + (size_t)b * L, (int)L);
     const size_t from = (size_t)b * L * row;
-    const size_t n = from >= emb_bytes ? 0 : std::min(len * row, emb_bytes - from);
-    if (n) memcpy(plan->emb_host.data() + from, (const uint8_t *)emb + from, n);
+    const size_t given = from >= emb_bytes ? 0 : (emb_bytes - from) / row;
+    plan->avail[b] = (int32_t)std::min(len, given);
+    plan->up_cu[b + 1] = plan->up_cu[b] + plan->avail[b];
   }
+  plan->pin_up.ensure(std::max<size_t>((size_t)plan->up_cu[plan->B] * row, 16));
+  for (int b = 0; b < plan->B; b++)
+    if (plan->avail[b])
+      memcpy((char *)plan->pin_up.p + (size_t)plan->up_cu[b] * row, (const uint8_t *)emb + (size_t)b * L * row,
+             (size_t)plan->avail[b] * row);
+  plan->up_rows = (const uint8_t *)plan->pin_up.p;
   plan->by_ids = false;
   KH_API_END
 }
