@@ -176,10 +176,27 @@ attn_kernel(AttnArgs a, Packing p) {
   // second half of the next one's: each sub-tile computes one block and carries it to the next.
   // The carry into the first sub-tile is computed here.
   [[maybe_unused]] float16v c2p_carry;
+  // p2c rows likewise: the A operands (pos_query rows of the distances) of a sub-tile's upper 32-row
+  // block are those of the previous sub-tile's lower block, so each sub-tile loads one block of
+  // position rows and carries it (f16; the f32 fragments of a block take 32 registers, and f32
+  // loads both blocks)
+  constexpr bool PQC = REL && sizeof(T) == 2;
+  typedef typename MF::frag frag_t;
+  auto pq_frags = [&](int d0, frag_t (&f)[QS], auto from_lds_t) {
+    int di = d0 + (lane & 31) + a.lmax - 1;  // this lane's distance row
+    di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
+    // < nb: the relidx table is checked against the tables
+    const int pr = decltype(from_lds_t)::value ? (int)sBucket[di] : a.bucket[di];
+    const T *pt = (const T *)a.pos_query + pr * hd + h * Dr;
+#pragma unroll
+    for (int s = 0; s < QS; s++) f[s] = load_frag<T, PAD>(pt, s * MF::KSTEP + g * MF::KLANE, Dr);
+  };
+  [[maybe_unused]] frag_t pq_carry[QS];
   if constexpr (REL) {
     // visible to every wavefront after the first K/V staging barrier
     for (int i = t; i < 2 * a.lmax - 1; i += 128) sBucket[i] = (short)a.bucket[i];
     c2p_carry = c2p_block(q0 + w * 32 - (klo + 31) + 32, std::false_type{});
+    if constexpr (PQC) pq_frags(q0 + w * 32 - (klo + 31) + 32, pq_carry, std::false_type{});
   }
 
   for (int kb = klo; kb < khi; kb += KT) {
@@ -257,21 +274,29 @@ attn_kernel(AttnArgs a, Packing p) {
           constexpr bool P2C = decltype(p2c_t)::value;
           [[maybe_unused]] float16v c2p_lo;
           if constexpr (!P2C) c2p_lo = c2p_block(dlo, std::true_type{});
+          [[maybe_unused]] frag_t pq_lo[QS];
+          if constexpr (P2C && PQC) pq_frags(dlo, pq_lo, std::true_type{});
 #pragma unroll
           for (int mt = 0; mt < 2; mt++) {
             float16v c = {};
             if constexpr (P2C) {
-              int di = dlo + (lane & 31) + mt * 32 + a.lmax - 1;  // this lane's distance row
-              di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
-              const int pr = sBucket[di];  // < nb: the relidx table is checked against the tables
-              const T *pt = (const T *)a.pos_query + pr * hd + h * Dr;
+              [[maybe_unused]] const T *pt = nullptr;
+              if constexpr (!PQC) {
+                int di = dlo + (lane & 31) + mt * 32 + a.lmax - 1;  // this lane's distance row
+                di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
+                const int pr = sBucket[di];  // < nb: the relidx table is checked against the tables
+                pt = (const T *)a.pos_query + pr * hd + h * Dr;
+              }
 #pragma unroll
               for (int s = 0; s < QS; s++) {
                 typename MF::frag kf;
                 if constexpr (sizeof(T) == 2) kf = *reinterpret_cast<const half8v *>(krow + s * MF::KSTEP);
                 else kf = krow[s * MF::KSTEP];
+                frag_t pf;
+                if constexpr (PQC) pf = mt == 0 ? pq_lo[s] : pq_carry[s];
+                else pf = load_frag<T, PAD>(pt, s * MF::KSTEP + g * MF::KLANE, Dr);
                 // [m][key]: lane = key
-                c = MF::mma(load_frag<T, PAD>(pt, s * MF::KSTEP + g * MF::KLANE, Dr), kf, c);
+                c = MF::mma(pf, kf, c);
               }
             } else {
               c = mt == 0 ? c2p_lo : c2p_carry;  // [m][query]: lane = query
@@ -285,6 +310,9 @@ attn_kernel(AttnArgs a, Packing p) {
             }
           }
           if constexpr (!P2C) c2p_carry = c2p_lo;
+          if constexpr (P2C && PQC)
+#pragma unroll
+            for (int s = 0; s < QS; s++) pq_carry[s] = pq_lo[s];
           const float *base = P2C ? sw + (lane & 31) + 31 + 4 * g * (RP - 1) : sw + (lane & 31) * (RP + 1) - 4 * g;
 #pragma unroll
           for (int r = 0; r < 16; r++) {
