@@ -125,6 +125,7 @@ attn_kernel(AttnArgs a, Packing p) {
   const int64_t base = tile.z;
   const int n = tile.w;
   const int64_t rs = (int64_t)3 * H * Dr;  // qkv row stride
+  const int rs32 = 3 * H * Dr;
   const T *qkv = (const T *)a.qkv;
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -199,22 +200,26 @@ attn_kernel(AttnArgs a, Packing p) {
     if constexpr (PQC) pq_frags(q0 + w * 32 - (klo + 31) + 32, pq_carry, std::false_type{});
   }
 
+  // this head's K and V columns in the sequence's first row
+  const T *k_seq = qkv + base * rs + (H + h) * Dr;
+  const T *v_seq = k_seq + H * Dr;
   for (int kb = klo; kb < khi; kb += KT) {
-    // K tile [key][d] and V tile transposed [d][key]; rows past khi are zero. A thread moves one
-    // 16-byte chunk of 4 consecutive keys: K rows as they are, V as 4-key vectors per d.
+    // K tile [key][d] and V tile transposed [d][key]. A thread moves one 16-byte chunk of 4
+    // consecutive keys: K rows as they are, V as 4-key vectors per d, from one row offset per chunk
+    // and no branch. Keys past khi load the sequence's last key instead: finite values whose
+    // scores are masked and whose weights are exactly 0, so they add nothing to the output.
     for (int c = t; c < (KT / 4) * CPR; c += 128) {
       const int kr = (c / CPR) * 4, dc = (c % CPR) * CE;
+      const int j0 = kb + kr;
+      const int last = khi - 1 - j0;  // the chunk's last key that exists (u <= last)
+      const int64_t off = (int64_t)j0 * rs + dc;
       uint4 kv[4], vv[4];
 #pragma unroll
       for (int u = 0; u < 4; u++) {
-        const int j = kb + kr + u;
-        kv[u] = make_uint4(0, 0, 0, 0);
-        vv[u] = make_uint4(0, 0, 0, 0);
-        if (j < khi) {
-          const T *row = qkv + (base + j) * rs;
-          kv[u] = load_chunk<T, PAD>(row + (H + h) * Dr, dc, Dr);
-          vv[u] = load_chunk<T, PAD>(row + (2 * H + h) * Dr, dc, Dr);
-        }
+        // (a row stride times at most 3 keys: 32-bit)
+        const int du = (u < last ? u : last) * rs32;
+        kv[u] = load_chunk<T, PAD>(k_seq + off + du, 0, Dr - dc);
+        vv[u] = load_chunk<T, PAD>(v_seq + off + du, 0, Dr - dc);
       }
 #pragma unroll
       for (int u = 0; u < 4; u++) *reinterpret_cast<uint4 *>(&sK[(kr + u) * LDK + dc]) = kv[u];
