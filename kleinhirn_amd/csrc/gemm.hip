@@ -629,7 +629,69 @@ __device__ __forceinline__ void lean_store(const GemmArgs &g, const char *lds, i
   auto chunk_at = [&](int row, int cc) {
     return *reinterpret_cast<const half8v *>(lds + row * RB + ((cc + row) % CPR) * 16);
   };
-  if constexpr (EPI == EPI_GEGLU) {
+  if constexpr (EPI == EPI_LN) {
+    // C = LayerNorm(residual + product) over whole rows (the tile spans the row: n0 = 0, N = BN).
+    // LPR lanes per row, PER 16-byte chunks per lane (lane l holds chunks k LPR + l): the lanes,
+    // the order of the sums and the shuffles of the separate MODE 2 LayerNorm over such rows, so
+    // both give the same bits. A row's lanes are LPR consecutive threads; every thread runs the
+    // same number of rows, so each shuffle has all its lanes.
+    constexpr int PER = 3, LPR = BN / (8 * PER);
+    static_assert(LPR * PER * 8 == BN && (LPR & (LPR - 1)) == 0 && NT % LPR == 0 && ROWS % (NT / LPR) == 0,
+                  "whole rows of 3 chunks per lane, a power-of-two lane group");
+    const half_t *res = (const half_t *)g.ln_res, *gam = (const half_t *)g.ln_g, *bet = (const half_t *)g.ln_b;
+    const int l = threadIdx.x % LPR;
+    auto group_sum = [&](float x) {
+#pragma unroll
+      for (int o = LPR / 2; o > 0; o >>= 1) x += __shfl_xor(x, o);
+      return x;
+    };
+#pragma unroll 1
+    for (int row = threadIdx.x / LPR; row < ROWS; row += NT / LPR) {
+      const int grow = grow0 + row;
+      const bool live = grow < g.M;  // the same for the row's lanes
+      float v[PER][8];
+#pragma unroll
+      for (int k = 0; k < PER; k++) {
+        const int cc = k * LPR + l;
+        const half8v pr = chunk_at(row, cc);
+        half8v ra = {};
+        if (live) ra = *reinterpret_cast<const half8v *>(res + (int64_t)grow * g.N + cc * 8);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          v[k][i] = (float)ra[i];
+          v[k][i] += (float)pr[i];
+        }
+      }
+      float sm = 0.f;
+#pragma unroll
+      for (int k = 0; k < PER; k++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) sm += v[k][i];
+      const float mean = group_sum(sm) / (float)g.N;
+      float sq = 0.f;
+#pragma unroll
+      for (int k = 0; k < PER; k++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const float d = v[k][i] - mean;
+          sq += d * d;
+        }
+      const float var = group_sum(sq) / (float)g.N;
+      const float inv = 1.0f / sqrtf(var + g.ln_eps);
+      if (live) {
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+          const int e0 = (k * LPR + l) * 8;
+          float gm[8], bt[8], y[8];
+          VecIO<half_t, 8>::load(gam + e0, gm);
+          if (bet) VecIO<half_t, 8>::load(bet + e0, bt);
+#pragma unroll
+          for (int i = 0; i < 8; i++) y[i] = (v[k][i] - mean) * inv * gm[i] + (bet ? bt[i] : 0.f);
+          VecIO<half_t, 8>::store(C + (int64_t)grow * g.ldc + e0, y);
+        }
+      }
+    }
+  } else if constexpr (EPI == EPI_GEGLU) {
     // output columns n0 / 2 .. n0 / 2 + BN / 2 of C [M, N / 2]: gelu(a) * b, a and b as stored
     constexpr int HC = CPR / 2;
     const int I = g.N / 2;
@@ -990,6 +1052,13 @@ void launch_act(const GemmArgs &g, hipStream_t s) {
     return;
   }
   const bool lean = sizeof(T) == 2 && lean_ok(g);
+  if constexpr (sizeof(T) == 2) {
+    // residual + LayerNorm over whole rows: 128 x 384 tiles (384 = the row; gemm_epi_ok checks)
+    if (g.epi == EPI_LN) {
+      launch_lean_epi<128, 384, 2, 4, ACT, EPI_LN, 2>(g, s);
+      return;
+    }
+  }
   int cfg = pick_tile(g, lean);
   if (cfg >= 5 && cfg <= 7 && g.batch > 1) cfg = 3;  // the persistent kernels walk one matrix
   if constexpr (sizeof(T) == 2) {
@@ -1040,6 +1109,8 @@ bool gemm_epi_ok(bool f16, const GemmArgs &g) {
              g.rope_cols <= g.N && g.rope_cols % g.rope_d == 0;
     case EPI_RESADD:
       return g.act == 0;
+    case EPI_LN:  // rows of exactly one 384-wide tile
+      return g.N == 384 && g.ldc == g.N;
     default:
       return false;
   }

@@ -51,13 +51,17 @@ struct GemmArgs {
   //  EPI_ROPE: rotate-half RoPE on the first rope_cols columns (q and k), head dim rope_d, table
   //            [L][cos D | sin D] at the row's position row_pos[m]
   //  EPI_RESADD: C += product (C is the residual stream, updated in place)
+  //  EPI_LN: C = LayerNorm(ln_res + product) over whole rows (gamma ln_g, beta ln_b, may be null;
+  //          eps ln_eps), the MODE 2 LayerNorm of the separate step with its lanes and sums
   // each applied to the product rounded to the storage type, as the separate ops read it
   int epi = 0;
   const float *rope_table = nullptr;
   const int32_t *row_pos = nullptr;
   int rope_cols = 0, rope_d = 0;
+  const void *ln_res = nullptr, *ln_g = nullptr, *ln_b = nullptr;
+  float ln_eps = 0.f;
 };
-enum { EPI_NONE = 0, EPI_GEGLU = 1, EPI_ROPE = 2, EPI_RESADD = 3 };
+enum { EPI_NONE = 0, EPI_GEGLU = 1, EPI_ROPE = 2, EPI_RESADD = 3, EPI_LN = 4 };
 void gemm(bool f16, const GemmArgs &g, hipStream_t s);
 // true when the MFMA tile kernel runs this shape (else the wave-per-output kernel)
 bool gemm_uses_mfma(bool f16, const GemmArgs &g);

@@ -137,13 +137,14 @@ struct Step {
   std::string name, kernel;
   bool seq_rows = false;  // fixed dispatch: one row per sequence (or rows_fixed rows)
   int64_t rows_fixed = 0;
-  Ref in[6];
+  Ref in[7];
   int N = 0, K = 0, act = 0, mode = 0, I = 0, H = 0, D = 0, window = 0, offset = 0, maxpos = 1, posids = 0;
   int Kmk = 1;  // gather markers per sequence
   float eps = 0.f, scale = 1.f;
   bool rel = false;
   std::string markers_id;  // gather: the init buffer holding the markers
-  int epi = 0;             // S_GEMM: fused step (EPI_*); in[4] holds a RoPE table
+  int epi = 0;             // S_GEMM: fused step (EPI_*); in[4] holds a RoPE table, or with EPI_LN the
+                           // residual (in[5], in[6]: the norm's gamma and beta; eps)
   int maskmul = 0;         // S_EMBLN: the output rows times the mask (MASKMUL)
   bool first_tiles = false;  // S_ATTN: only the first query tile of each sequence
 };
@@ -560,16 +561,17 @@ static bool dead_after(const std::vector<Step> &steps, size_t from, const std::s
   for (size_t i = from; i < steps.size(); i++) {
     const Step &s = steps[i];
     const int wo = write_only_slot(s);
-    for (int k = 0; k < 6; k++)
+    for (int k = 0; k < (int)(sizeof(s.in) / sizeof(s.in[0])); k++)
       if (k != wo && s.in[k].id == id) return false;
     if (wo >= 0 && s.in[wo].id == id) return true;
   }
   return true;
 }
 
-// GEMM + GeGLU, GEMM + RoPE and GEMM + residual add run as one launch when the lean kernel takes
-// the shape (the fused op is applied to the product rounded to the storage type, so results match
-// the separate ops); the intermediate buffer then needs no memory.
+// GEMM + GeGLU, GEMM + RoPE, GEMM + residual add and GEMM + residual LayerNorm (MODE 2 over
+// 384-wide rows, one tile per row) run as one launch when the lean kernel takes the shape (the
+// fused op is applied to the product rounded to the storage type, so results match the separate
+// ops); the intermediate buffer then needs no memory.
 static void fuse_steps(kh_plan *pl) {
   std::vector<Step> &st = pl->steps;
   std::vector<Step> out;
@@ -616,6 +618,17 @@ static void fuse_steps(kh_plan *pl) {
           fused.in[3] = n.in[0];
           fused.name = s.name + "+" + n.name;
         }
+      } else if (n.kind == S_LN && n.mode == 2 && n.in[1].id == c && n.in[0].id != c && n.N == s.N &&
+                 n.in[0].id != pl->in_emb && c != pl->out_buf && dead_after(st, i + 2, c)) {
+        g.epi = EPI_LN;
+        if ((ok = gemm_epi_ok(pl->f16, g))) {
+          fused.epi = EPI_LN;
+          fused.in[3] = n.in[5];
+          fused.in[4] = n.in[0];
+          fused.in[5] = n.in[2];
+          fused.in[6] = n.in[3];
+          fused.eps = n.eps;
+        }
       }
       if (ok) {
         if (fused.epi != EPI_RESADD) fused.name = s.name + "+" + n.name;
@@ -646,6 +659,7 @@ static bool row_uses(const Step &s, std::vector<RowUse> &u) {
       if (s.epi == EPI_ROPE || !is_w(s.in[1].id) || !is_w(s.in[2].id)) return false;
       u.push_back({0, s.K, true, false});
       u.push_back({3, s.epi == EPI_GEGLU ? s.N / 2 : s.N, s.epi == EPI_RESADD, true});
+      if (s.epi == EPI_LN) u.push_back({4, s.N, true, false});
       return true;
     case S_LN:
       u.push_back({0, s.N, true, false});
@@ -833,6 +847,12 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook, const 
         g.rope_d = s.D;
       } else if (s.epi == EPI_RESADD) {
         out_elems *= 2;
+      } else if (s.epi == EPI_LN) {
+        g.ln_res = bufp(pl, s.in[4]);
+        g.ln_g = bufp(pl, s.in[5]);
+        g.ln_b = bufp(pl, s.in[6]);
+        g.ln_eps = s.eps;
+        out_elems = 2.0 * rows * s.N + 2.0 * s.N;  // the residual read, the rows written, gamma and beta
       }
       begin(gemm_uses_mfma(f16, g) ? "gemm_mfma" : "gemm_rowdot", 2.0 * rows * s.N * s.K,
             (double)es * ((double)rows * s.K + (double)s.N * s.K + out_elems + (g.bias ? s.N : 0)));

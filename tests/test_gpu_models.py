@@ -152,6 +152,39 @@ def test_fused_products_with_biases_match_separate_ops(monkeypatch):
     assert np.array_equal(fused, separate), np.abs(fused - separate).max()
 
 
+def _layernorm_launches(case, f16=True):
+    """Outputs and the number of LayerNorm launches of one forward of the case's batch plan."""
+    from kleinhirn_amd.backend import HipBackend
+    W = configs.storage(case.weights, f16)
+    be = HipBackend(W)
+    r = be.runner(build_plan(case.spec, case.head, case.length, len(case.ids), f16))
+    r.upload(inputs.run_input(case.spec, W["embeddings.word.weight"], case.ids, case.length))
+    r.trace(True)
+    r.run(case.length * len(case.ids))
+    out = r.read_output().reshape(len(case.ids), -1)
+    launches = r.trace_read()
+    r.trace(False)
+    r.destroy()
+    be.dispose()
+    return out, sum(1 for l in launches if l["kernel"] == "layernorm")
+
+
+def test_fused_residual_layernorm_matches_separate_ops(monkeypatch):
+    """XLM-R MiniLM (post-LN, 384-wide rows): the out projection and FFN out run with the residual
+    + LayerNorm (MODE 2) in the product's epilogue, one 128 x 384 tile per row band, the lanes,
+    sums and shuffles of the separate LayerNorm; with fusion off (KH_NO_FUSION) the separate
+    kernels run. The outputs are identical, and the fused forward launches no LayerNorm of its own
+    (the embedding's runs in the embedding kernel)."""
+    case, ref = case_and_oracle("c5")
+    fused, n_fused = _layernorm_launches(case)
+    monkeypatch.setenv("KH_NO_FUSION", "1")
+    separate, n_separate = _layernorm_launches(case)
+    print(f"LayerNorm launches fused {n_fused}, separate {n_separate}; max |d| {np.abs(fused - separate).max():.3e}")
+    assert n_separate == n_fused + 2 * case.spec["layers"], (n_fused, n_separate)
+    assert np.array_equal(fused, separate)
+    assert cosine_rows(ref, fused).min() >= 0.999
+
+
 @pytest.mark.parametrize("key", ["c2", "c3b", "c4", "c5"])
 def test_cls_tail_on_sequence_rows_equals_full_forward(monkeypatch, key):
     """A pooled-CLS head reads row 0 of each sequence after the last attention, so the runner runs
