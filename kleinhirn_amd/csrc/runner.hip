@@ -1183,8 +1183,9 @@ constexpr size_t PREFETCH_MIN = 256 * 1024;
 // (PrefetchArgs: its threads read them after their rows), so those products find them in the
 // memory-side cache: a layer's weights come cold from HBM otherwise, which costs a product up to
 // a quarter of its time when the weights are a sizeable part of its operands (c2: 14 MB of
-// weights per layer against 20 MB rows). Products whose weights are under an eighth of their row
-// operand (c4, c5) gain nothing and are left out.
+// weights per layer against 20 MB rows, FFN out's 4.7 MB against 79 MB). Products whose weights
+// are under a 32nd of their row operand (c4, c5: under 1 MB against hundreds) gain nothing and
+// are left out.
 static PrefetchArgs prefetch_for(kh_plan *pl, const std::vector<Step> &steps, size_t i) {
   PrefetchArgs a;
   int r = 0;
@@ -1194,7 +1195,7 @@ static PrefetchArgs prefetch_for(kh_plan *pl, const std::vector<Step> &steps, si
     if (s.kind != S_GEMM || s.seq_rows) continue;
     const size_t es = pl->f16 ? 2 : 4;
     const size_t bytes = (size_t)s.N * s.K * es;
-    if (bytes < PREFETCH_MIN || bytes * 8 < (size_t)pl->T * s.K * es) continue;
+    if (bytes < PREFETCH_MIN || bytes * 32 < (size_t)pl->T * s.K * es) continue;
     a.p[r] = bufp(pl, s.in[1]);
     a.n16[r] = (int64_t)(bytes / 16);
     a.total += a.n16[r];
