@@ -1024,8 +1024,13 @@ int pick_tile(const GemmArgs &g, bool lean) {
     // 78 for 192 x 128, so the k loop is no longer bound by the loads into LDS. It wins where the
     // product's K is short (<= 768) and the rows are many (c5's products +5-7 % each, c5 +2 % end
     // to end). At c2's size (and its two halves of ~6,400 rows on two streams) one block per CU
-    // fills the chip worse than two of 192 x 128: c2 lost 1.6 % with it on the QKV product.
+    // filled the chip worse than two of 192 x 128 in an earlier build: c2 lost 1.6 % with it on
+    // the QKV product. With every product's weights prefetched and the halves launched
+    // interleaved, the QKV product (no activation, N >= 2304) of c2's size and of its halves gains
+    // with it: c2 +1.1 % (c3a, 16k rows, keeps 128 x 384, which divides its rows into whole rounds).
     if (g.K <= 768 && g.M >= 65536) return 14;
+    if (g.K <= 768 && g.M >= 4096 && g.M <= 13312 && g.act == 0 && g.epi == EPI_NONE && g.N >= 2304 && g.N % 256 == 0)
+      return 14;
     // very many rows (c5's 1.2M): per-tile efficiency decides, measured on the 384-wide models:
     // 128 x 384 for 384- and 768-wide outputs (one column tile: each A band is read once), 192 x 256
     // for wider ones fed by a short K
