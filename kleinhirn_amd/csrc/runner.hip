@@ -1178,6 +1178,10 @@ static int64_t env_int(const char *name, int64_t dflt);
 // bytes of a product's weight matrix worth a prefetch (below this the product's own first reads
 // are a small part of it)
 constexpr size_t PREFETCH_MIN = 256 * 1024;
+// rows below which a forward is bound by its launches' latency (c1: 128 rows): its products read
+// their weights once anyway, and a prefetch would only move that read into the LayerNorm (a c1
+// forward took 0.93 ms with it against 0.58 ms without)
+constexpr int64_t PREFETCH_MIN_ROWS = 2048;
 
 // A LayerNorm over the packed rows carries the weights of the products up to the next LayerNorm
 // (PrefetchArgs: its threads read them after their rows), so those products find them in the
@@ -1188,6 +1192,7 @@ constexpr size_t PREFETCH_MIN = 256 * 1024;
 // are left out.
 static PrefetchArgs prefetch_for(kh_plan *pl, const std::vector<Step> &steps, size_t i) {
   PrefetchArgs a;
+  if (pl->T < PREFETCH_MIN_ROWS) return a;
   int r = 0;
   for (size_t j = i + 1; j < steps.size() && r < PREFETCH_RANGES; j++) {
     const Step &s = steps[j];
