@@ -32,13 +32,14 @@ PEAK = {"f16_mfma_tflops": 2500.0, "f32_mfma_tflops": 157.3, "hbm_gbs": 8000.0}
 # bench (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch averaged over the family), each counter scaled
 # by what it reads for a plain device copy of 1 GiB (python3 -m kleinhirn_amd.profiling copy 1024:
 # FETCH_SIZE reads 0.5 GiB -> x2.0, WRITE_SIZE reads 1.0 GiB -> x1.0). Summaries with the commands:
-# profiles/gemm_mfma_c2_roberta_base_ragged256_traffic.md and layernorm_c5_xlmr_minilm_l12_pairs4096_traffic.md.
+# profiles/gemm_mfma_c2_roberta_base_ragged256_traffic.md, gemm_mfma_c5_xlmr_minilm_l12_pairs4096_traffic.md and
+# layernorm_c4_modernbert_small_b64_traffic.md.
 # Re-measured whenever the kernel changes (an entry whose source digest differs is not reported).
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
 TRAFFIC_KIB = {  # (workload, family): (FETCH_SIZE KiB, WRITE_SIZE KiB) per dispatch, kernel source sha256[:16]
-    ("c2-roberta-base-f16-ragged256", "gemm_mfma"): (56630.3, 40025.3, "7f81084289178b4b"),
-    ("c5-xlmr-minilm-l12-f16-pairs4096", "gemm_mfma"): (917770.3, 1894393.1, "7f81084289178b4b"),
-    ("c5-xlmr-minilm-l12-f16-pairs4096", "layernorm"): (834323.0, 834276.7, "22b73117ffec2da0"),
+    ("c2-roberta-base-f16-ragged256", "gemm_mfma"): (51032.5, 40025.3, "114e313b732a7714"),
+    ("c5-xlmr-minilm-l12-f16-pairs4096", "gemm_mfma"): (1118271.8, 1894393.1, "114e313b732a7714"),
+    ("c4-modernbert-small-f16-b64", "layernorm"): (93671.7, 187261.4, "22b73117ffec2da0"),
 }
 # the source file of each kernel family (a counter figure measured on other code is not reported)
 FAMILY_SOURCE = {"gemm_mfma": "gemm.hip", "attention": "attention.hip", "layernorm": "rowops.hip",
