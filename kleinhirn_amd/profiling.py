@@ -5,6 +5,7 @@ HIP-event timings and PMC byte counters can be set against a launch's algorithmi
     python3 -m kleinhirn_amd.profiling copy <MiB>            plain device copy (counter calibration)
     python3 -m kleinhirn_amd.profiling trace <rocprof dir>   kernel-trace summary by family and by kernel (markdown)
     python3 -m kleinhirn_amd.profiling pmc <rocprof dir> ... counter sums per family (markdown)
+    python3 -m kleinhirn_amd.profiling clock <rocprof dir>   shader clock per kernel of a --pmc GRBM_COUNT run (markdown)
 
 The copy mode is the calibration workload: FETCH_SIZE and WRITE_SIZE of one copy of N bytes should
 read N bytes each; the ratio is the scale applied to the same counters of the encoder's kernels.
@@ -144,6 +145,31 @@ def pmc_summary(dirs: list[str]) -> str:
     return "\n".join(lines)
 
 
+def clock_table(d: str, xcds: int = 8, top: int = 12) -> str:
+    """Shader clock per kernel (template instance and grid) from a `--pmc GRBM_COUNT` run. The
+    counter sums the GPU clock over the XCDs for the dispatch's sampling window, which is longer
+    than the kernel's timestamps by a fixed amount; the window of the runtime's 2 us copy kernels
+    (median) estimates it. GHz = (count - that) / duration / XCDs: a kernel's average clock while it
+    ran, meaningful where the kernel is long against the correction (median over its dispatches)."""
+    rows = [r for r in _csv_rows(d, "counter_collection.csv") if r["Counter_Name"] == "GRBM_COUNT"]
+    base = sorted(float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"])
+    fixed = base[len(base) // 2] if base else 0.0
+    per = collections.defaultdict(list)
+    for r in rows:
+        ns = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+        if ns <= 0 or "rocclr" in r["Kernel_Name"]:
+            continue
+        grid = r.get("Grid_Size") or "x".join(r.get(f"Grid_Size_{a}", "?") for a in "XYZ")
+        per[(short_name(r["Kernel_Name"]), grid)].append((ns, (float(r["Counter_Value"]) - fixed) / ns / xcds))
+    lines = [f"window correction: {fixed:.0f} counts (median of the runtime copy kernels)", "",
+             "| kernel | grid (work-items) | dispatches | median us | median GHz |", "|---|---|---|---|---|"]
+    for (name, grid), v in sorted(per.items(), key=lambda kv: -sum(x[0] for x in kv[1]))[:top]:
+        ns = sorted(x[0] for x in v)[len(v) // 2]
+        ghz = sorted(x[1] for x in v)[len(v) // 2]
+        lines.append(f"| {name} | {grid} | {len(v)} | {ns / 1e3:.1f} | {ghz:.2f} |")
+    return "\n".join(lines)
+
+
 def copy_probe(mib: int, reps: int = 3) -> None:
     import torch
     n = mib << 20
@@ -166,6 +192,8 @@ def main(argv: list[str]) -> int:
         print(kernel_table(argv[1]))
     elif len(argv) >= 2 and argv[0] == "pmc":
         print(pmc_summary(argv[1:]))
+    elif len(argv) >= 2 and argv[0] == "clock":
+        print(clock_table(argv[1]))
     else:
         print(__doc__, file=sys.stderr)
         return 2
