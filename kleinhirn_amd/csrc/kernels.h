@@ -90,8 +90,6 @@ struct PrefetchArgs {
   const void *p[PREFETCH_RANGES] = {};
   int64_t n16[PREFETCH_RANGES] = {};
   int64_t total = 0;
-  uint32_t *sink = nullptr;
-  int never = 0;
 };
 
 struct EmbLnArgs {

@@ -17,8 +17,8 @@ constexpr int ROWS_PER_BLOCK = 4;  // wavefronts (rows) per 256-thread block
 // The weight prefetch a LayerNorm launch carries (PrefetchArgs): after its rows are stored, every
 // thread of the grid reads its share of the ranges' 16-byte pieces (piece g, g + threads, ...), so
 // the reads wait on nothing and the launch ends about one memory latency later. The XOR of the
-// words is stored only when `never` is set, which the host never does; the compiler cannot drop
-// the loads.
+// words is handed to an empty asm statement, so the compiler cannot drop the loads, and nothing is
+// written.
 __device__ __forceinline__ void prefetch_share(const PrefetchArgs &pf) {
   if (pf.total <= 0) return;
   const int64_t nth = (int64_t)gridDim.x * blockDim.x;
@@ -33,7 +33,7 @@ __device__ __forceinline__ void prefetch_share(const PrefetchArgs &pf) {
     const uint4 v = ((const uint4 *)pf.p[r])[off];
     acc ^= v.x ^ v.y ^ v.z ^ v.w;
   }
-  if (pf.never) pf.sink[0] = acc;
+  asm volatile("" ::"v"(acc));
 }
 
 // Per lane: PER groups of VEC contiguous elements; group g = k * 64 + lane.

@@ -200,8 +200,6 @@ struct kh_plan {
   hipStream_t stream = nullptr;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   bool ran = false;
-  // the never-written word of the LayerNorm kernels' weight prefetch
-  DevMem pf_sink;
 
   // A small batch runs as two halves on two streams: sequences [0, split) here, [split, B) on the
   // twin (the same plan, its own buffers and stream), so the kernels of one half fill the CUs the
@@ -1205,10 +1203,6 @@ static PrefetchArgs prefetch_for(kh_plan *pl, const std::vector<Step> &steps, si
     a.n16[r] = (int64_t)(bytes / 16);
     a.total += a.n16[r];
     r++;
-  }
-  if (r > 0) {
-    if (!pl->pf_sink.p) pl->pf_sink.alloc(256);
-    a.sink = (uint32_t *)pl->pf_sink.p;
   }
   return a;
 }
