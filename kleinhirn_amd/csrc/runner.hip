@@ -1409,7 +1409,9 @@ static void launch_forward(kh_plan *pl, int rows, const LaunchHook &hook, bool s
     const bool pf = env_int("KH_NO_PREFETCH", 0) == 0;
     auto step = [&](kh_plan *p, const std::vector<Step> &st, size_t i) {
       const bool ln = (st[i].kind == S_LN || st[i].kind == S_EMBLN) && !st[i].seq_rows;
-      exec_step(p, st[i], hook, pf && ln ? prefetch_for(p, st, i) : PrefetchArgs());
+      // (the halves run in step, so the twin's products find the weights this plan's LayerNorms
+      // brought in: only this plan's carry the prefetch; c2 +0.8 %)
+      exec_step(p, st[i], hook, pf && ln && p == pl ? prefetch_for(p, st, i) : PrefetchArgs());
     };
     for (size_t i = 0; i < std::max(s1.size(), s2.size()); i++) {
       if (i < s1.size()) step(pl, s1, i);
