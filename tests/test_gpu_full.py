@@ -130,3 +130,16 @@ def test_split_full_batch_is_deterministic(monkeypatch):
         assert np.array_equal(o, whole), (i, int((np.abs(o - whole).max(1) > 0).sum()))
     d = decision_parity(ref, whole)
     assert d["mismatched"] == 0, d
+
+
+def test_weight_prefetch_leaves_results_unchanged(monkeypatch):
+    """The whole c2 batch (12,801 rows: the LayerNorms carry the next products' weights) equals the
+    run with the prefetch off (KH_NO_PREFETCH=1) bit for bit, and the oracle's decisions. The
+    prefetch only reads the weights, in bounds, and writes nothing."""
+    case, ref = full_case("c2_full")
+    with_pf = hip_outputs(case, f16=True)
+    monkeypatch.setenv("KH_NO_PREFETCH", "1")
+    without = hip_outputs(case, f16=True)
+    assert np.array_equal(with_pf, without), int((np.abs(with_pf - without).max(1) > 0).sum())
+    d = decision_parity(ref, with_pf)
+    assert d["mismatched"] == 0, d
