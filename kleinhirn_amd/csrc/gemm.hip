@@ -566,6 +566,54 @@ __global__ void __launch_bounds__(256) gemm_rowdot_kernel(GemmArgs g) {
 }
 
 
+// f32 products of a few hundred rows (too few rows for 128 x 128 tiles: a short sequence, a CLS
+// tail), on v_mfma_f32_32x32x2f32: one 32 x 32 output tile per block of four wavefronts. The K
+// range is split in four contiguous quarters, one per wavefront, whose sums are added through LDS
+// in a fixed order (((w0 + w1) + w2) + w3), so a tile's result does not depend on M or on the other
+// tiles. Each lane loads 16-byte row pieces of A and W: the lane of row l % 32 and half h = l / 32
+// takes elements h and h + 2 of each 4-element piece (k = 4q + h, then 4q + 2 + h: the k index the
+// MFMA's lane h half holds). Rows past M load row M - 1 and are not stored. Needs K % 16 == 0,
+// N % 32 == 0, 16-byte aligned rows (small_f32_ok).
+template <int ACT>
+__global__ void __launch_bounds__(256) gemm_small_f32_kernel(GemmArgs g, int tiles_n) {
+  __shared__ float red[3][16][64];  // wavefronts 1..3's sums, [register][lane]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int z = blockIdx.z;
+  const int m0 = (blockIdx.x / tiles_n) * 32, n0 = (blockIdx.x % tiles_n) * 32;
+  const int r = lane & 31, h = lane >> 5;
+  const int mrow = m0 + r < g.M ? m0 + r : g.M - 1;
+  const float *a = (const float *)g.a + (int64_t)z * g.a_bs + (int64_t)mrow * g.lda;
+  const float *w = (const float *)g.w + (int64_t)z * g.w_bs + (int64_t)(n0 + r) * g.ldw;
+  const int kq = g.K / 4, k0 = wave * kq, k1 = k0 + kq;
+  float16v acc = {};
+#pragma unroll 4
+  for (int k = k0; k < k1; k += 4) {
+    const float4v x = *reinterpret_cast<const float4v *>(a + k);
+    const float4v y = *reinterpret_cast<const float4v *>(w + k);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(h ? x[1] : x[0], h ? y[1] : y[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(h ? x[3] : x[2], h ? y[3] : y[2], acc, 0, 0, 0);
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) red[wave - 1][i][lane] = acc[i];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int p = 0; p < 3; p++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] += red[p][i][lane];
+  // register 4 q + e is row 8 q + 4 h + e of the tile, column r
+  const int n = n0 + r;
+  const float b = g.bias ? ((const float *)g.bias)[n] : 0.f;
+  float *c = (float *)g.c + (int64_t)z * g.c_bs;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int m = m0 + 8 * (i >> 2) + 4 * h + (i & 3);
+    if (m < g.M) c[(int64_t)m * g.ldc + n] = act_fn<ACT>(acc[i] + b);
+  }
+}
+
 // Lean f16 kernel: the same slab ring as gemm_dma_kernel (two stages, direct-to-LDS loads,
 // swizzled 128-byte rows) with the per-tile and per-slab vector-ALU work cut down, since with two
 // blocks per CU every VALU slot competes with the other block's MFMAs:
@@ -1131,11 +1179,31 @@ bool gemm_uses_mfma(bool f16, const GemmArgs &g) {
          g.w_bs % ce == 0 && aligned16(g.a) && aligned16(g.w);
 }
 
+// f32 products the small-tile MFMA kernel takes (those gemm_uses_mfma leaves to the wavefront-per-
+// output kernel, with whole 32-column tiles and 4-element k pieces per wavefront quarter)
+static bool small_f32_ok(bool f16, const GemmArgs &g) {
+  return !f16 && !g.rowdot && g.epi == EPI_NONE && !gemm_uses_mfma(f16, g) && g.N % 32 == 0 && g.K % 16 == 0 &&
+         g.lda % 4 == 0 && g.ldw % 4 == 0 && g.a_bs % 4 == 0 && g.w_bs % 4 == 0 && aligned16(g.a) &&
+         aligned16(g.w);
+}
+
+bool gemm_on_mfma(bool f16, const GemmArgs &g) { return gemm_uses_mfma(f16, g) || small_f32_ok(f16, g); }
+
 void gemm(bool f16, const GemmArgs &g, hipStream_t s) {
   if (g.M <= 0 || g.N <= 0 || g.batch <= 0) return;
   if (gemm_uses_mfma(f16, g)) {
     if (f16) launch_mfma<half_t>(g, s);
     else launch_mfma<float>(g, s);
+  } else if (small_f32_ok(f16, g)) {
+    const int tn = g.N / 32;
+    dim3 grid((unsigned)(((g.M + 31) / 32) * tn), 1, (unsigned)g.batch);
+    switch (g.act) {
+      case 1: launch((gemm_small_f32_kernel<1>), grid, dim3(256), 0, s, g, tn); break;
+      case 2: launch((gemm_small_f32_kernel<2>), grid, dim3(256), 0, s, g, tn); break;
+      case 3: launch((gemm_small_f32_kernel<3>), grid, dim3(256), 0, s, g, tn); break;
+      case 4: launch((gemm_small_f32_kernel<4>), grid, dim3(256), 0, s, g, tn); break;
+      default: launch((gemm_small_f32_kernel<0>), grid, dim3(256), 0, s, g, tn); break;
+    }
   } else {
     const int64_t waves = (int64_t)g.M * ((g.N + 3) / 4);
     dim3 grid((unsigned)((waves + 3) / 4), 1, (unsigned)g.batch);

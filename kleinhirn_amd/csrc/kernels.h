@@ -65,6 +65,8 @@ enum { EPI_NONE = 0, EPI_GEGLU = 1, EPI_ROPE = 2, EPI_RESADD = 3, EPI_LN = 4 };
 void gemm(bool f16, const GemmArgs &g, hipStream_t s);
 // true when the MFMA tile kernel runs this shape (else the wave-per-output kernel)
 bool gemm_uses_mfma(bool f16, const GemmArgs &g);
+// the product runs on MFMA (the tiled kernels, or for a few hundred f32 rows the 32 x 32 one)
+bool gemm_on_mfma(bool f16, const GemmArgs &g);
 // true when g's fused step (g.epi) can run inside the product for this shape and storage type
 bool gemm_epi_ok(bool f16, const GemmArgs &g);
 

@@ -852,7 +852,7 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook, const 
         g.ln_eps = s.eps;
         out_elems = 2.0 * rows * s.N + 2.0 * s.N;  // the residual read, the rows written, gamma and beta
       }
-      begin(gemm_uses_mfma(f16, g) ? "gemm_mfma" : "gemm_rowdot", 2.0 * rows * s.N * s.K,
+      begin(gemm_on_mfma(f16, g) ? "gemm_mfma" : "gemm_rowdot", 2.0 * rows * s.N * s.K,
             (double)es * ((double)rows * s.K + (double)s.N * s.K + out_elems + (g.bias ? s.N : 0)));
       gemm(f16, g, st);
       end();

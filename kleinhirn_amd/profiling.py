@@ -26,6 +26,7 @@ FAMILIES = [
     ("gemm_dma_kernel", "gemm_mfma"),
     ("gemm_persist_kernel", "gemm_mfma"),
     ("gemm_reg_kernel", "gemm_mfma"),
+    ("gemm_small_f32_kernel", "gemm_mfma"),
     ("gemm_rowdot_kernel", "gemm_rowdot"),
     ("attn_kernel", "attention"),
     ("embln_kernel", "embln"),
