@@ -118,7 +118,8 @@ attn_kernel(AttnArgs a, Packing p) {
   // items (head, query tile), tiles fastest: the query tiles of one sequence and head run
   // together on one XCD and find its K and V rows in that XCD's L2
   const int H = a.H;
-  const int item = xcd_tile(blockIdx.x, a.ntiles * H);
+  const int item = a.work ? a.work[blockIdx.x] : xcd_tile(blockIdx.x, a.ntiles * H);
+  if (item < 0) return;  // (the work list's padding: an XCD with fewer items)
   const int4 tile = a.tiles[item % a.ntiles];
   const int q0 = tile.y;
   const int h = item / a.ntiles;
@@ -460,7 +461,7 @@ attn_kernel(AttnArgs a, Packing p) {
 
 template <typename T, bool REL, bool WIN>
 void launch_w(const AttnArgs &a, const Packing &p, hipStream_t s) {
-  dim3 grid((unsigned)(a.ntiles * a.H));
+  dim3 grid((unsigned)(a.work ? a.nwork : a.ntiles * a.H));
   // the relative path's bucket table: 2 lmax - 1 16-bit entries of dynamic LDS
   const unsigned dyn = REL ? (unsigned)((2 * a.lmax - 1) * sizeof(short) + 3) / 4 * 4 : 0;
   // head dimensions 32 and 64 as they are; others padded to the next of the two (up to 64)

@@ -155,6 +155,10 @@ struct AttnArgs {
   int lmax = 0;
   const int4 *tiles;
   int ntiles;
+  // the grid's blocks in dispatch order (null: item = xcd_tile(block)): block b runs item work[b]
+  // (item h * ntiles + tile; -1 for none), its blocks' XCD b % 8 (see the runner's attention order)
+  const int32_t *work = nullptr;
+  int nwork = 0;
 };
 void attention(bool f16, const AttnArgs &a, const Packing &p, hipStream_t s);
 constexpr int ATTN_QTILE = 64;
