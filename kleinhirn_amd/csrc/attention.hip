@@ -184,21 +184,29 @@ attn_kernel(AttnArgs a, Packing p) {
   // loads both blocks)
   constexpr bool PQC = REL && sizeof(T) == 2;
   typedef typename MF::frag frag_t;
-  auto pq_frags = [&](int d0, frag_t (&f)[QS], auto from_lds_t) {
+  // the position rows (of `table`) of the distance block starting at d0, as MFMA A fragments
+  auto pos_frags = [&](const void *table, int d0, frag_t (&f)[QS], auto from_lds_t) {
     int di = d0 + (lane & 31) + a.lmax - 1;  // this lane's distance row
     di = di < 0 ? 0 : (di > 2 * a.lmax - 2 ? 2 * a.lmax - 2 : di);
     // < nb: the relidx table is checked against the tables
     const int pr = decltype(from_lds_t)::value ? (int)sBucket[di] : a.bucket[di];
-    const T *pt = (const T *)a.pos_query + pr * hd + h * Dr;
+    const T *pt = (const T *)table + pr * hd + h * Dr;
 #pragma unroll
     for (int s = 0; s < QS; s++) f[s] = load_frag<T, PAD>(pt, s * MF::KSTEP + g * MF::KLANE, Dr);
   };
   [[maybe_unused]] frag_t pq_carry[QS];
+  // f16: the pos_key rows of the next sub-tile's c2p block are loaded one sub-tile ahead (its
+  // distances are the current ones minus 32), so their L2 latency passes under the current
+  // sub-tile's work instead of stalling its c2p products
+  [[maybe_unused]] frag_t pk_next[QS];
   if constexpr (REL) {
     // visible to every wavefront after the first K/V staging barrier
     for (int i = t; i < 2 * a.lmax - 1; i += 128) sBucket[i] = (short)a.bucket[i];
     c2p_carry = c2p_block(q0 + w * 32 - (klo + 31) + 32, std::false_type{});
-    if constexpr (PQC) pq_frags(q0 + w * 32 - (klo + 31) + 32, pq_carry, std::false_type{});
+    if constexpr (PQC) {
+      pos_frags(a.pos_query, q0 + w * 32 - (klo + 31) + 32, pq_carry, std::false_type{});
+      pos_frags(a.pos_key, q0 + w * 32 - (klo + 31), pk_next, std::false_type{});
+    }
   }
 
   // this head's K and V columns in the sequence's first row
@@ -279,9 +287,16 @@ attn_kernel(AttnArgs a, Packing p) {
         auto term = [&](auto p2c_t) {
           constexpr bool P2C = decltype(p2c_t)::value;
           [[maybe_unused]] float16v c2p_lo;
-          if constexpr (!P2C) c2p_lo = c2p_block(dlo, std::true_type{});
+          if constexpr (!P2C && PQC) {
+            c2p_lo = float16v{};
+#pragma unroll
+            for (int s = 0; s < QS; s++) c2p_lo = MF::mma(pk_next[s], qf[s], c2p_lo);
+            pos_frags(a.pos_key, dlo - 32, pk_next, std::true_type{});
+          } else if constexpr (!P2C) {
+            c2p_lo = c2p_block(dlo, std::true_type{});
+          }
           [[maybe_unused]] frag_t pq_lo[QS];
-          if constexpr (P2C && PQC) pq_frags(dlo, pq_lo, std::true_type{});
+          if constexpr (P2C && PQC) pos_frags(a.pos_query, dlo, pq_lo, std::true_type{});
 #pragma unroll
           for (int mt = 0; mt < 2; mt++) {
             float16v c = {};
