@@ -86,7 +86,7 @@ struct Packing {
 
 // Ranges (16-byte pieces) a LayerNorm launch reads and discards after its rows: the weights of the
 // products that follow it, brought into the memory-side cache just before they run. total is the
-// sum of n16; sink is a device word the kernels never write (never is 0).
+// sum of n16; nothing is written.
 constexpr int PREFETCH_RANGES = 4;
 struct PrefetchArgs {
   const void *p[PREFETCH_RANGES] = {};
