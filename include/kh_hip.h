@@ -144,6 +144,9 @@ int kh_sched_destroy(kh_sched *s);
 #define KH_SCORES_SIGMOID 1 /* multi-label: 1 / (1 + e^-logit), label = argmax of the logits */
 #define KH_SCORES_RAW 2     /* regression: the logits, label = their argmax */
 #define KH_SCORES_L2 3      /* embeddings: rows divided by max(|row|, 1e-12) */
+#define KH_SCORES_OPTIONS 4 /* Julia's option probabilities: softmax with the exponentials summed and divided
+                             * in double, one rounding per value (softmaxPrefix, src/julia.ts:57-65); pass the
+                             * first min(markers, options) logits of a row as its columns; label = argmax */
 
 /* Scores of a row-major [rows, cols] f32 array in the reference's arithmetic (f32 values,
  * double operations, one rounding to f32; softmax, l2normalize, argmaxRows with ties to the

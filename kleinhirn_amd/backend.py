@@ -34,7 +34,7 @@ EXPORTS = [
 ]
 
 # kh_scores kinds
-SCORES_SOFTMAX, SCORES_SIGMOID, SCORES_RAW, SCORES_L2 = 0, 1, 2, 3
+SCORES_SOFTMAX, SCORES_SIGMOID, SCORES_RAW, SCORES_L2, SCORES_OPTIONS = 0, 1, 2, 3, 4
 
 # kh_load_manifest / kh_manifest_check flags
 LOAD_NO_SHA256, LOAD_CHECK_ROWS, LOAD_NO_WORDS = 1, 2, 4

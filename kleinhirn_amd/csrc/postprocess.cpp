@@ -41,6 +41,15 @@ void row_scores(const float *in, int32_t cols, int kind, float *out, int32_t *in
       if (index) *index = argmax(out, cols);
       break;
     }
+    case KH_SCORES_OPTIONS: {  // softmaxPrefix (src/julia.ts:57-65): no f32 store before the sum
+      double mx = -INFINITY;
+      for (int32_t i = 0; i < cols; i++) mx = std::max(mx, (double)in[i]);
+      double sum = 0;
+      for (int32_t i = 0; i < cols; i++) sum += std::exp((double)in[i] - mx);
+      for (int32_t i = 0; i < cols; i++) out[i] = (float)(std::exp((double)in[i] - mx) / sum);
+      if (index) *index = argmax(out, cols);
+      break;
+    }
     case KH_SCORES_SIGMOID:  // multi-label: 1 / (1 + e^-v), the label of the largest logit
       for (int32_t i = 0; i < cols; i++) out[i] = (float)(1.0 / (1.0 + std::exp(-(double)in[i])));
       if (index) *index = argmax(in, cols);

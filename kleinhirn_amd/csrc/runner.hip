@@ -2308,7 +2308,7 @@ int kh_read_output(kh_plan *plan, float *out, size_t count) {
 }
 
 static void scores_of(const float *logits, int64_t rows, int32_t cols, int kind, float *scores, int32_t *index) {
-  if (kind < KH_SCORES_SOFTMAX || kind > KH_SCORES_L2) fail(KH_EINVAL, "scores kind " + std::to_string(kind));
+  if (kind < KH_SCORES_SOFTMAX || kind > KH_SCORES_OPTIONS) fail(KH_EINVAL, "scores kind " + std::to_string(kind));
   if (rows < 0 || cols <= 0) fail(KH_EINVAL, "scores of " + std::to_string(rows) + " x " + std::to_string(cols));
   if (rows && (!logits || !scores)) fail(KH_EINVAL, "null argument");
   const int64_t bad = post::count_nonfinite(logits, rows * cols);

@@ -60,6 +60,9 @@ export const SCORES_SOFTMAX = 0;
 export const SCORES_SIGMOID = 1;
 export const SCORES_RAW = 2;
 export const SCORES_L2 = 3;
+// Julia's option probabilities (softmaxPrefix, src/julia.ts:57-65): pass the first
+// min(markers, options) logits as one row
+export const SCORES_OPTIONS = 4;
 
 // kh_manifest_info (include/kh_hip.h)
 export interface ManifestInfo {

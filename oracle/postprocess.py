@@ -9,10 +9,12 @@ float operation followed, where the reference stores into a Float32Array, by a r
   each stored value / sum stored f32;
 * sigmoid of the multi-label classify (src/encoder.ts:506-507): 1 / (1 + e^-x) stored f32;
 * l2normalize (src/tasks.ts:35-42): double sum of squares, max(sqrt, 1e-12), x / norm stored f32;
+* softmaxPrefix of the Julia head's option logits (src/julia.ts:57-65): max, a double sum of
+  e^(x - max) with nothing stored in between, each e^(x - max) / sum stored f32;
 * argmaxRows (src/tasks.ts:72-84): strict '>' scan, ties to the lower index;
 * rerank order (src/encoder.ts:541): by score descending, then index.
 Pinned by the reference's own vectors (tests/tasks.test.ts:5-32 of the reference) in
-tests/test_scores.py.
+tests/test_scores.py; softmax_prefix, which no reference test covers, by closed forms there.
 """
 from __future__ import annotations
 
@@ -20,7 +22,7 @@ import math
 
 import numpy as np
 
-SOFTMAX, SIGMOID, RAW, L2 = 0, 1, 2, 3
+SOFTMAX, SIGMOID, RAW, L2, OPTIONS = 0, 1, 2, 3, 4
 
 
 def f32(x: float) -> float:
@@ -36,6 +38,16 @@ def softmax(row) -> list[float]:
     for o in out:
         s += o
     return [f32(o / s) for o in out]
+
+
+def softmax_prefix(row) -> list[float]:
+    mx = -math.inf
+    for v in row:
+        mx = max(mx, float(v))
+    s = 0.0
+    for v in row:
+        s += math.exp(float(v) - mx)
+    return [f32(math.exp(float(v) - mx) / s) for v in row]
 
 
 def sigmoid(row) -> list[float]:
@@ -70,6 +82,9 @@ def scores(logits: np.ndarray, kind: int) -> tuple[np.ndarray, np.ndarray]:
     for r, row in enumerate(logits.tolist()):
         if kind == SOFTMAX:
             s = softmax(row)
+            idx[r] = argmax(s)
+        elif kind == OPTIONS:
+            s = softmax_prefix(row)
             idx[r] = argmax(s)
         elif kind == SIGMOID:
             s = sigmoid(row)

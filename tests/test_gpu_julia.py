@@ -1,7 +1,7 @@
 """Julia decision head through the C ABI (kh_upload_qtypes, kh_upload_markers, f32 logits)
 against the oracle on the same seeded encoder, weights, payloads and qtypes. Bars: f32 logits
 within 1e-3, masked slots exactly -1e4, f16 within 2e-2; a batch plan equals single plans; a
-qtype past the type table is an error."""
+qtype past the type table is an error; the option probabilities after the head within 1e-3."""
 from __future__ import annotations
 
 import numpy as np
@@ -66,6 +66,24 @@ def test_julia_f32_matches_oracle(batch_plan):
     m = masked(packed)
     assert m.any() and np.all(got[m] == np.float32(-1e4))
     assert np.abs(got[~m] - ref[~m]).max() <= 1e-3, np.abs(got[~m] - ref[~m]).max()
+
+
+def test_julia_option_probabilities():
+    """The step after the head (src/julia.ts:224-227): softmaxPrefix over each sequence's first
+    min(markers, options) logits, kh_scores KH_SCORES_OPTIONS on the HIP logits against the oracle's
+    restatement on the oracle logits."""
+    from kleinhirn_amd import backend as B
+    from oracle import postprocess as P
+    ids, W, packed, qtypes, ref = reference()
+    got = hip_logits(ids, W, packed, qtypes, False)
+    m = masked(packed)
+    for i in range(len(ids)):
+        valid = int((~m[i]).sum())
+        assert valid > 0 and not m[i, :valid].any(), "the live slots are a prefix"
+        probs, label = B.scores(got[i, :valid], B.SCORES_OPTIONS)
+        want = np.array(P.softmax_prefix(ref[i, :valid].tolist()), np.float32)
+        assert np.abs(probs[0] - want).max() <= 1e-3 and abs(float(probs[0].sum()) - 1) < 1e-5
+        assert label[0] == int(np.argmax(want)) or np.sort(want)[-1] - np.sort(want)[-2] < 1e-3
 
 
 def test_julia_f16_matches_oracle_and_single_plans():

@@ -38,6 +38,27 @@ def test_oracle_closed_forms():
     assert P.rank([0.5, 2.0, 0.5, -1.0]) == [1, 0, 2, 3]
 
 
+def test_option_softmax_closed_forms():
+    """Julia's option probabilities (softmaxPrefix, src/julia.ts:57-65) where the exact value is
+    known, and where it parts from the tasks softmax (which stores each exponential as f32 before
+    the sum)."""
+    assert P.softmax_prefix([0.0, 0.0, 0.0, 0.0]) == [0.25] * 4
+    want = [1 / 6, 2 / 6, 3 / 6]
+    got = P.softmax_prefix([0.0, math.log(2.0), math.log(3.0)])
+    assert all(abs(g - w) < 6e-8 for g, w in zip(got, want)), got
+    assert P.softmax_prefix([-1e4, 0.0]) == [0.0, 1.0]  # e^-10000 underflows: one option takes all
+    assert P.softmax_prefix([7.5]) == [1.0]
+    # the sum of the unrounded exponentials: the two softmaxes differ in the last bit on some rows
+    x = (RNG.standard_normal((2000, 5)) * 3).astype(np.float32)
+    diff = 0
+    for row in x.tolist():
+        a, b = P.softmax_prefix(row), P.softmax(row)
+        assert max(abs(u - v) for u, v in zip(a, b)) <= 1.2e-7
+        assert abs(sum(a) - 1) < 1e-6
+        diff += a != b
+    assert diff > 0
+
+
 def test_library_matches_the_reference_vectors():
     s, i = B.scores(np.array([[1, 2, 3]], np.float32))
     assert abs(s[0, 2] - 0.6652409557748219) < 1e-6 and i[0] == 2
@@ -49,7 +70,7 @@ def test_library_matches_the_reference_vectors():
     assert i.tolist() == [1, 0]
 
 
-@pytest.mark.parametrize("kind", [B.SCORES_SOFTMAX, B.SCORES_SIGMOID, B.SCORES_RAW, B.SCORES_L2])
+@pytest.mark.parametrize("kind", [B.SCORES_SOFTMAX, B.SCORES_SIGMOID, B.SCORES_RAW, B.SCORES_L2, B.SCORES_OPTIONS])
 def test_library_equals_oracle_bit_for_bit(kind):
     for rows, cols in [(256, 3), (64, 384), (4096, 1), (7, 2)]:
         x = (RNG.standard_normal((rows, cols)) * 4).astype(np.float32)
