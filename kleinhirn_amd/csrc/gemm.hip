@@ -633,13 +633,14 @@ __device__ __forceinline__ rsrc_t panel_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// Lean epilogue, staging half: bias, activation and the f16 conversion of this wavefront's
-// accumulators, written row-major into `lds` (rows of BN values, 16-byte chunks rotated by the row).
-// acc[i][j][4 q + e] is row row0 + 32 i, column wn TN + 32 j + 8 q + 4 lg + e of the staged rows.
-template <int BN, int WN, int ACT, int EPI, int FM, int FN>
-__device__ __forceinline__ void lean_stage(const GemmArgs &g, float16v (&acc)[FM][FN], char *lds, int n0, int wn,
-                                           int lane, int row0) {
-  constexpr int TN = BN / WN, RB = BN * 2, CPR = BN / 8;
+// The bias values of this wavefront's accumulator columns, loaded once before the k loop so the
+// epilogue waits for no load: bv[j][q] holds the 4 values of columns wn TN + 32 j + 8 q + 4 lg
+// (+ 0..3), or for GeGLU those of the rows of W the tile's two halves take (columns n0 / 2 + c of
+// each half of the product). Columns past N read column 0 and are zeroed: every lane loads, so
+// the loads go out together instead of one conditional load (and its wait) per column group.
+template <int BN, int WN, int EPI, int FN>
+__device__ __forceinline__ void lean_bias(const GemmArgs &g, int n0, int wn, int lane, half4v (&bv)[FN][4]) {
+  constexpr int TN = BN / WN;
   const int lg = lane >> 5;
   const half_t *bias = (const half_t *)g.bias;
 #pragma unroll
@@ -647,15 +648,32 @@ __device__ __forceinline__ void lean_stage(const GemmArgs &g, float16v (&acc)[FM
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const int nl = wn * TN + j * 32 + 8 * q;
-      // bias column of these 4 values: the tile's columns, or for GeGLU the rows of W its two
-      // halves take (columns n0 / 2 + c of each half of the product)
       int n = n0 + nl + 4 * lg;
       if constexpr (EPI == EPI_GEGLU) n = (nl < BN / 2 ? (n0 >> 1) + nl : g.N / 2 + (n0 >> 1) + nl - BN / 2) + 4 * lg;
-      float b[4] = {0.f, 0.f, 0.f, 0.f};
-      if (bias && n < g.N) {
-        const half4v bv = *reinterpret_cast<const half4v *>(bias + n);
-        b[0] = (float)bv[0]; b[1] = (float)bv[1]; b[2] = (float)bv[2]; b[3] = (float)bv[3];
+      half4v b = {};
+      if (bias) {
+        b = *reinterpret_cast<const half4v *>(bias + (n < g.N ? n : 0));
+        if (n >= g.N) b = half4v{};
       }
+      bv[j][q] = b;
+    }
+}
+
+// Lean epilogue, staging half: bias, activation and the f16 conversion of this wavefront's
+// accumulators, written row-major into `lds` (rows of BN values, 16-byte chunks rotated by the row).
+// acc[i][j][4 q + e] is row row0 + 32 i, column wn TN + 32 j + 8 q + 4 lg + e of the staged rows;
+// bv[j][q] holds its bias values (lean_bias).
+template <int BN, int WN, int ACT, int EPI, int FM, int FN>
+__device__ __forceinline__ void lean_stage(const GemmArgs &g, float16v (&acc)[FM][FN], const half4v (&bv)[FN][4],
+                                           char *lds, int wn, int lane, int row0) {
+  constexpr int TN = BN / WN, RB = BN * 2, CPR = BN / 8;
+  const int lg = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < FN; j++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int nl = wn * TN + j * 32 + 8 * q;
+      const float b[4] = {(float)bv[j][q][0], (float)bv[j][q][1], (float)bv[j][q][2], (float)bv[j][q][3]};
 #pragma unroll
       for (int i = 0; i < FM; i++) {
         const int ml = row0 + i * 32;
@@ -668,6 +686,105 @@ __device__ __forceinline__ void lean_stage(const GemmArgs &g, float16v (&acc)[FM
     }
 }
 
+// EPI_LN rows (C = LayerNorm(residual + product) over whole rows: the tile spans the row, n0 = 0,
+// N = BN). LPR lanes per row, PER 16-byte chunks per lane (lane l holds chunks k LPR + l): the
+// lanes, the order of the sums and the shuffles of the separate MODE 2 LayerNorm over such rows,
+// so both give the same bits. A row's lanes are LPR consecutive threads; the NT threads take RPP
+// rows per pass, NP passes, so each shuffle has all its lanes.
+template <int ROWS, int BN, int NW>
+struct LnRows {
+  static constexpr int PER = 3, LPR = BN / (8 * PER), NT = 64 * NW, RPP = NT / LPR, NP = ROWS / RPP;
+  static_assert(LPR * PER * 8 == BN && (LPR & (LPR - 1)) == 0 && NT % LPR == 0 && ROWS % RPP == 0,
+                "whole rows of 3 chunks per lane, a power-of-two lane group");
+  half8v res[NP][PER];  // this thread's residual chunks, pass p, chunk k
+  half8v gam[PER], bet[PER];  // its chunks of gamma and beta (the same in every pass)
+};
+
+// The residual chunks of every pass and the gamma and beta chunks, loaded before the tile is
+// staged: their latency is paid once per tile, where loads in each pass waited once per pass.
+template <int ROWS, int BN, int NW>
+__device__ __forceinline__ void ln_preload(const GemmArgs &g, int grow0, LnRows<ROWS, BN, NW> &lr) {
+  typedef LnRows<ROWS, BN, NW> R;
+  const half_t *res = (const half_t *)g.ln_res;
+  const int l = threadIdx.x % R::LPR;
+#pragma unroll
+  for (int k = 0; k < R::PER; k++) {
+    const int e0 = (k * R::LPR + l) * 8;
+    lr.gam[k] = *reinterpret_cast<const half8v *>((const half_t *)g.ln_g + e0);
+    lr.bet[k] = g.ln_b ? *reinterpret_cast<const half8v *>((const half_t *)g.ln_b + e0) : half8v{};
+  }
+#pragma unroll
+  for (int p = 0; p < R::NP; p++) {
+    const int grow = grow0 + (int)threadIdx.x / R::LPR + p * R::RPP;
+#pragma unroll
+    for (int k = 0; k < R::PER; k++) {
+      half8v ra = {};
+      if (grow < g.M) ra = *reinterpret_cast<const half8v *>(res + (int64_t)grow * g.N + (k * R::LPR + l) * 8);
+      lr.res[p][k] = ra;
+    }
+  }
+}
+
+template <int ROWS, int BN, int NW>
+__device__ __forceinline__ void lean_store_ln(const GemmArgs &g, const char *lds, int grow0,
+                                              const LnRows<ROWS, BN, NW> &lr) {
+  typedef LnRows<ROWS, BN, NW> R;
+  constexpr int PER = R::PER, LPR = R::LPR, RB = BN * 2, CPR = BN / 8;
+  half_t *C = (half_t *)g.c;
+  const bool beta = g.ln_b != nullptr;
+  const int l = threadIdx.x % LPR;
+  auto group_sum = [&](float x) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+  };
+#pragma unroll
+  for (int p = 0; p < R::NP; p++) {
+    const int row = (int)threadIdx.x / LPR + p * R::RPP;
+    const int grow = grow0 + row;
+    const bool live = grow < g.M;  // the same for the row's lanes
+    float v[PER][8];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const int cc = k * LPR + l;
+      const half8v pr = *reinterpret_cast<const half8v *>(lds + row * RB + ((cc + row) % CPR) * 16);
+      const half8v ra = lr.res[p][k];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        v[k][i] = (float)ra[i];
+        v[k][i] += (float)pr[i];
+      }
+    }
+    float sm = 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; k++)
+#pragma unroll
+      for (int i = 0; i < 8; i++) sm += v[k][i];
+    const float mean = group_sum(sm) / (float)g.N;
+    float sq = 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; k++)
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float d = v[k][i] - mean;
+        sq += d * d;
+      }
+    const float var = group_sum(sq) / (float)g.N;
+    const float inv = 1.0f / sqrtf(var + g.ln_eps);
+    if (live) {
+#pragma unroll
+      for (int k = 0; k < PER; k++) {
+        const int e0 = (k * LPR + l) * 8;
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+          y[i] = (v[k][i] - mean) * inv * (float)lr.gam[k][i] + (beta ? (float)lr.bet[k][i] : 0.f);
+        VecIO<half_t, 8>::store(C + (int64_t)grow * g.ldc + e0, y);
+      }
+    }
+  }
+}
+
 // Lean epilogue, store half: ROWS staged rows (row r is C row grow0 + r) leave as whole 16-byte
 // chunks, through the fused step of EPI; NT threads share the rows.
 template <int ROWS, int BN, int NW, int EPI>
@@ -677,69 +794,7 @@ __device__ __forceinline__ void lean_store(const GemmArgs &g, const char *lds, i
   auto chunk_at = [&](int row, int cc) {
     return *reinterpret_cast<const half8v *>(lds + row * RB + ((cc + row) % CPR) * 16);
   };
-  if constexpr (EPI == EPI_LN) {
-    // C = LayerNorm(residual + product) over whole rows (the tile spans the row: n0 = 0, N = BN).
-    // LPR lanes per row, PER 16-byte chunks per lane (lane l holds chunks k LPR + l): the lanes,
-    // the order of the sums and the shuffles of the separate MODE 2 LayerNorm over such rows, so
-    // both give the same bits. A row's lanes are LPR consecutive threads; every thread runs the
-    // same number of rows, so each shuffle has all its lanes.
-    constexpr int PER = 3, LPR = BN / (8 * PER);
-    static_assert(LPR * PER * 8 == BN && (LPR & (LPR - 1)) == 0 && NT % LPR == 0 && ROWS % (NT / LPR) == 0,
-                  "whole rows of 3 chunks per lane, a power-of-two lane group");
-    const half_t *res = (const half_t *)g.ln_res, *gam = (const half_t *)g.ln_g, *bet = (const half_t *)g.ln_b;
-    const int l = threadIdx.x % LPR;
-    auto group_sum = [&](float x) {
-#pragma unroll
-      for (int o = LPR / 2; o > 0; o >>= 1) x += __shfl_xor(x, o);
-      return x;
-    };
-#pragma unroll 1
-    for (int row = threadIdx.x / LPR; row < ROWS; row += NT / LPR) {
-      const int grow = grow0 + row;
-      const bool live = grow < g.M;  // the same for the row's lanes
-      float v[PER][8];
-#pragma unroll
-      for (int k = 0; k < PER; k++) {
-        const int cc = k * LPR + l;
-        const half8v pr = chunk_at(row, cc);
-        half8v ra = {};
-        if (live) ra = *reinterpret_cast<const half8v *>(res + (int64_t)grow * g.N + cc * 8);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          v[k][i] = (float)ra[i];
-          v[k][i] += (float)pr[i];
-        }
-      }
-      float sm = 0.f;
-#pragma unroll
-      for (int k = 0; k < PER; k++)
-#pragma unroll
-        for (int i = 0; i < 8; i++) sm += v[k][i];
-      const float mean = group_sum(sm) / (float)g.N;
-      float sq = 0.f;
-#pragma unroll
-      for (int k = 0; k < PER; k++)
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const float d = v[k][i] - mean;
-          sq += d * d;
-        }
-      const float var = group_sum(sq) / (float)g.N;
-      const float inv = 1.0f / sqrtf(var + g.ln_eps);
-      if (live) {
-#pragma unroll
-        for (int k = 0; k < PER; k++) {
-          const int e0 = (k * LPR + l) * 8;
-          float gm[8], bt[8], y[8];
-          VecIO<half_t, 8>::load(gam + e0, gm);
-          if (bet) VecIO<half_t, 8>::load(bet + e0, bt);
-#pragma unroll
-          for (int i = 0; i < 8; i++) y[i] = (v[k][i] - mean) * inv * gm[i] + (bet ? bt[i] : 0.f);
-          VecIO<half_t, 8>::store(C + (int64_t)grow * g.ldc + e0, y);
-        }
-      }
-    }
-  } else if constexpr (EPI == EPI_GEGLU) {
+  if constexpr (EPI == EPI_GEGLU) {
     // output columns n0 / 2 .. n0 / 2 + BN / 2 of C [M, N / 2]: gelu(a) * b, a and b as stored
     constexpr int HC = CPR / 2;
     const int I = g.N / 2;
@@ -857,6 +912,8 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
   float16v acc[FM][FN];
   const int nk = g.K / 64;
   issue(0, 0);
+  half4v bv[FN][4];
+  lean_bias<BN, WN, EPI, FN>(g, n0, wn, lane, bv);
 
   auto slab = [&](const char *base, auto first_t) {
     constexpr bool first = decltype(first_t)::value;
@@ -949,9 +1006,19 @@ __device__ __forceinline__ void gemm_lean_body(const GemmArgs &g, int tiles_m, i
   // tile goes row-major into LDS (16-byte chunks of a row rotated by the row) and leaves as
   // whole 16-byte chunks
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  lean_stage<BN, WN, ACT, EPI>(g, acc, smem, n0, wn, lane, arow);
-  __syncthreads();
-  lean_store<BM, BN, NW, EPI>(g, smem, m0, n0);
+  if constexpr (EPI == EPI_LN) {
+    LnRows<BM, BN, NW> lr;
+    ln_preload<BM, BN, NW>(g, m0, lr);
+    lean_stage<BN, WN, ACT, EPI>(g, acc, bv, smem, wn, lane, arow);
+    // the staged rows are visible after this wavefront's LDS writes and the barrier; the residual
+    // loads stay in flight across it
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    lean_store_ln<BM, BN, NW>(g, smem, m0, lr);
+  } else {
+    lean_stage<BN, WN, ACT, EPI>(g, acc, bv, smem, wn, lane, arow);
+    __syncthreads();
+    lean_store<BM, BN, NW, EPI>(g, smem, m0, n0);
+  }
 }
 
 // (the body is a device function: the buffer-resource type exists only in device compilation)
