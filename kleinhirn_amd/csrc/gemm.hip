@@ -811,37 +811,74 @@ __device__ __forceinline__ void lean_store(const GemmArgs &g, const char *lds, i
       }
     }
   } else {
+    // IT chunks per thread, chunk q = threadIdx.x + it NT. The global reads of a fused step (the
+    // residual of RESADD; the positions and the cos/sin rows of RoPE) go out for BATCH chunks at a
+    // time from clamped, always valid addresses, before any of them is used: one wait per batch
+    // instead of one (or two) per chunk.
+    constexpr int IT = ROWS * CPR / NT;
+    static_assert(IT * NT == ROWS * CPR, "whole chunk rounds per thread");
+    constexpr int BATCH = EPI == EPI_ROPE ? (IT % 4 == 0 ? 4 : 1) : IT;
 #pragma unroll
-    for (int q = threadIdx.x; q < ROWS * CPR; q += NT) {
-      const int row = q / CPR, cc = q % CPR;
-      const int grow = grow0 + row, gcol = n0 + cc * 8;
-      if (grow < g.M && gcol < g.N) {
-        half8v x = chunk_at(row, cc);
-        half_t *dst = C + (int64_t)grow * g.ldc + gcol;
-        if constexpr (EPI == EPI_ROPE) {
-          // rotate-half on q and k: d < D / 2 pairs with d + D / 2 of the same head (tiles start
-          // at head boundaries); cos at table[pos][d], sin at table[pos][D + d]
-          if (gcol < g.rope_cols) {
-            const int D = g.rope_d, half = D >> 1;
-            const int d0 = gcol % D;
-            const bool lo = d0 < half;
-            const half8v y = chunk_at(row, lo ? cc + half / 8 : cc - half / 8);
-            const float *t = g.rope_table + (int64_t)g.row_pos[grow] * 2 * D + (lo ? d0 : d0 - half);
-            half8v o;
+    for (int b0 = 0; b0 < IT; b0 += BATCH) {
+      [[maybe_unused]] half8v res[BATCH];
+      [[maybe_unused]] float4v tc[BATCH][2], ts[BATCH][2];
+      if constexpr (EPI == EPI_RESADD) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-              const float c = t[e], sn = t[D + e];
-              o[e] = lo ? (half_t)((float)x[e] * c - (float)y[e] * sn) : (half_t)((float)x[e] * c + (float)y[e] * sn);
-            }
-            x = o;
-          }
-        } else if constexpr (EPI == EPI_RESADD) {
-          // residual += product, in f32, rounded once (the add op on the stored product)
-          const half8v r = *reinterpret_cast<const half8v *>(dst);
-#pragma unroll
-          for (int e = 0; e < 8; e++) x[e] = (half_t)((float)r[e] + (float)x[e]);
+        for (int u = 0; u < BATCH; u++) {
+          const int q = threadIdx.x + (b0 + u) * NT;
+          const int grow = grow0 + q / CPR, gcol = n0 + (q % CPR) * 8;
+          const bool live = grow < g.M && gcol < g.N;
+          res[u] = *reinterpret_cast<const half8v *>(live ? C + (int64_t)grow * g.ldc + gcol : C);
         }
-        *reinterpret_cast<half8v *>(dst) = x;
+      } else if constexpr (EPI == EPI_ROPE) {
+        // rotate-half on q and k: d < D / 2 pairs with d + D / 2 of the same head (tiles start
+        // at head boundaries); cos at table[pos][d], sin at table[pos][D + d]
+        const int D = g.rope_d, half = D >> 1;
+        int pos[BATCH];
+#pragma unroll
+        for (int u = 0; u < BATCH; u++) {
+          const int grow = grow0 + (int)(threadIdx.x + (b0 + u) * NT) / CPR;
+          pos[u] = g.row_pos[grow < g.M ? grow : 0];
+        }
+#pragma unroll
+        for (int u = 0; u < BATCH; u++) {
+          const int gcol = n0 + (int)((threadIdx.x + (b0 + u) * NT) % CPR) * 8;
+          const int d0 = gcol % D;
+          const float *t = g.rope_table + (int64_t)pos[u] * 2 * D + (d0 < half ? d0 : d0 - half);
+          tc[u][0] = *reinterpret_cast<const float4v *>(t);
+          tc[u][1] = *reinterpret_cast<const float4v *>(t + 4);
+          ts[u][0] = *reinterpret_cast<const float4v *>(t + D);
+          ts[u][1] = *reinterpret_cast<const float4v *>(t + D + 4);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < BATCH; u++) {
+        const int q = threadIdx.x + (b0 + u) * NT;
+        const int row = q / CPR, cc = q % CPR;
+        const int grow = grow0 + row, gcol = n0 + cc * 8;
+        if (grow < g.M && gcol < g.N) {
+          half8v x = chunk_at(row, cc);
+          half_t *dst = C + (int64_t)grow * g.ldc + gcol;
+          if constexpr (EPI == EPI_ROPE) {
+            if (gcol < g.rope_cols) {
+              const int D = g.rope_d, half = D >> 1;
+              const bool lo = gcol % D < half;
+              const half8v y = chunk_at(row, lo ? cc + half / 8 : cc - half / 8);
+              half8v o;
+#pragma unroll
+              for (int e = 0; e < 8; e++) {
+                const float c = tc[u][e >> 2][e & 3], sn = ts[u][e >> 2][e & 3];
+                o[e] = lo ? (half_t)((float)x[e] * c - (float)y[e] * sn) : (half_t)((float)x[e] * c + (float)y[e] * sn);
+              }
+              x = o;
+            }
+          } else if constexpr (EPI == EPI_RESADD) {
+            // residual += product, in f32, rounded once (the add op on the stored product)
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = (half_t)((float)res[u][e] + (float)x[e]);
+          }
+          *reinterpret_cast<half8v *>(dst) = x;
+        }
       }
     }
   }
