@@ -117,7 +117,16 @@ __global__ void __launch_bounds__(256) layernorm_kernel(const T *__restrict__ a,
 // Several rows per wavefront: a group of LPR lanes (a power of two) holds one row as PER 16-byte
 // chunks per lane, so every lane loads (a 768-wide f16 row: 32 lanes x 3 chunks, two rows per
 // wavefront) and the reductions stay inside the group.
-template <typename T, int LPR, int PER>
+// The 16-byte chunk c of a row as VEC floats.
+template <typename T, int VEC>
+__device__ __forceinline__ void chunk_to_float(const uint4 &c, float *o) {
+  T e[VEC];
+  __builtin_memcpy(e, &c, 16);
+#pragma unroll
+  for (int i = 0; i < VEC; i++) o[i] = (float)e[i];
+}
+
+template <typename T, int LPR, int PER, bool RES>
 __global__ void __launch_bounds__(256) layernorm_rows_kernel(const T *__restrict__ a, const T *__restrict__ b,
                                                              const T *__restrict__ gamma,
                                                              const T *__restrict__ beta, T *__restrict__ out,
@@ -133,14 +142,25 @@ __global__ void __launch_bounds__(256) layernorm_rows_kernel(const T *__restrict
     return;
   }
   const T *ar = a + (ids ? (int64_t)ids[r] : r) * N;
-  float v[PER][VEC];
+  // every chunk the row needs (a, the residual b when RES, gamma, beta) is requested before the
+  // first is used: one memory round trip per row instead of one per chunk
+  uint4 ca[PER], cb[PER], cg[PER], ct[PER];
+  const T *bt_src = beta ? beta : gamma;  // (gamma's chunks again without beta: never used)
 #pragma unroll
   for (int k = 0; k < PER; k++) {
     const int e0 = (k * LPR + l) * VEC;
-    VecIO<T, VEC>::load(ar + e0, v[k]);
-    if (b) {
+    ca[k] = *reinterpret_cast<const uint4 *>(ar + e0);
+    if constexpr (RES) cb[k] = *reinterpret_cast<const uint4 *>(b + r * N + e0);
+    cg[k] = *reinterpret_cast<const uint4 *>(gamma + e0);
+    ct[k] = *reinterpret_cast<const uint4 *>(bt_src + e0);
+  }
+  float v[PER][VEC];
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    chunk_to_float<T, VEC>(ca[k], v[k]);
+    if constexpr (RES) {
       float y[VEC];
-      VecIO<T, VEC>::load(b + r * N + e0, y);
+      chunk_to_float<T, VEC>(cb[k], y);
 #pragma unroll
       for (int i = 0; i < VEC; i++) v[k][i] += y[i];
     }
@@ -170,8 +190,8 @@ __global__ void __launch_bounds__(256) layernorm_rows_kernel(const T *__restrict
   for (int k = 0; k < PER; k++) {
     const int e0 = (k * LPR + l) * VEC;
     float gm[VEC], bt[VEC], y[VEC];
-    VecIO<T, VEC>::load(gamma + e0, gm);
-    if (beta) VecIO<T, VEC>::load(beta + e0, bt);
+    chunk_to_float<T, VEC>(cg[k], gm);
+    chunk_to_float<T, VEC>(ct[k], bt);
 #pragma unroll
     for (int i = 0; i < VEC; i++) y[i] = (v[k][i] - mean) * inv * gm[i] + (beta ? bt[i] : 0.f);
     if (row_scale) {
@@ -258,9 +278,13 @@ void layernorm_t(const void *a, const void *b, const void *gamma, const void *be
     auto go_rows = [&](auto lpr_t) {
       constexpr int LPR = decltype(lpr_t)::value;
       const int64_t per_block = (int64_t)ROWS_PER_BLOCK * (WAVE / LPR);
-      launch((layernorm_rows_kernel<T, LPR, 3>), dim3((unsigned)((rows + per_block - 1) / per_block)), dim3(256),
-             0, s, (const T *)a, (const T *)b, (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps, ids, pf,
-             row_scale);
+      const dim3 grid((unsigned)((rows + per_block - 1) / per_block));
+      if (b)
+        launch((layernorm_rows_kernel<T, LPR, 3, true>), grid, dim3(256), 0, s, (const T *)a, (const T *)b,
+               (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps, ids, pf, row_scale);
+      else
+        launch((layernorm_rows_kernel<T, LPR, 3, false>), grid, dim3(256), 0, s, (const T *)a, (const T *)b,
+               (const T *)gamma, (const T *)beta, (T *)out, rows, N, eps, ids, pf, row_scale);
     };
     switch (lpr) {
       case 8: go_rows(std::integral_constant<int, 8>()); return;
