@@ -78,6 +78,48 @@ __device__ __forceinline__ void ln_finish(float (&v)[PER][VEC], int N, const T *
   }
 }
 
+// ln_finish with gamma and beta already in registers (gm, bt; bt unused without beta): the same
+// operations in the same order.
+template <typename T, int VEC, int PER>
+__device__ __forceinline__ void ln_finish_pre(float (&v)[PER][VEC], int N, const float (&gm)[PER][VEC],
+                                              const float (&bt)[PER][VEC], bool beta, float eps, T *out, int lane,
+                                              const float *scale) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    int e0 = (k * WAVE + lane) * VEC;
+#pragma unroll
+    for (int i = 0; i < VEC; i++) s += (e0 + i < N) ? v[k][i] : 0.f;
+  }
+  float mean = wave_sum(s) / (float)N;
+  float sq = 0.f;
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    int e0 = (k * WAVE + lane) * VEC;
+#pragma unroll
+    for (int i = 0; i < VEC; i++) {
+      float d = v[k][i] - mean;
+      sq += (e0 + i < N) ? d * d : 0.f;
+    }
+  }
+  float var = wave_sum(sq) / (float)N;
+  float inv = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    int e0 = (k * WAVE + lane) * VEC;
+    if (e0 >= N) continue;
+    float y[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; i++) y[i] = (v[k][i] - mean) * inv * gm[k][i] + (beta ? bt[k][i] : 0.f);
+    if (scale) {
+      const float sc = *scale;
+#pragma unroll
+      for (int i = 0; i < VEC; i++) y[i] *= sc;
+    }
+    VecIO<T, VEC>::store(out + e0, y);
+  }
+}
+
 template <typename T, int VEC, int PER>
 __global__ void __launch_bounds__(256) layernorm_kernel(const T *__restrict__ a, const T *__restrict__ b,
                                                         const T *__restrict__ gamma, const T *__restrict__ beta,
@@ -222,24 +264,30 @@ __global__ void __launch_bounds__(256) embln_kernel(EmbLnArgs a, Packing p, Pref
   const T *word = a.word ? (const T *)a.word + r * N : (const T *)a.table + (int64_t)a.ids[r] * N;
   const T *pos = a.pos ? (const T *)a.pos + (int64_t)prow * N : nullptr;
   const T *typ = a.typ ? (const T *)a.typ + (int64_t)(t & 0xffffu) * N : nullptr;
+  // all of the row's reads go out before the first is used: no branch between them (absent tables
+  // and lanes past N read the word row's first chunk instead, unused), gamma and beta with them
+  const T *ps = pos ? pos : word, *ys = typ ? typ : word;
+  const T *gs = (const T *)a.gamma, *bs = a.beta ? (const T *)a.beta : gs;
+  float w[PER][VEC], q[PER][VEC], y[PER][VEC], gm[PER][VEC], bt[PER][VEC];
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    const int e0 = (k * WAVE + lane) * VEC;
+    const int ee = e0 < N ? e0 : 0;
+    VecIO<T, VEC>::load(word + ee, w[k]);
+    VecIO<T, VEC>::load(ps + ee, q[k]);
+    VecIO<T, VEC>::load(ys + ee, y[k]);
+    VecIO<T, VEC>::load(gs + ee, gm[k]);
+    VecIO<T, VEC>::load(bs + ee, bt[k]);
+  }
   float v[PER][VEC];
 #pragma unroll
   for (int k = 0; k < PER; k++) {
-    int e0 = (k * WAVE + lane) * VEC;
-    if (e0 < N) {
-      float w[VEC], q[VEC], y[VEC];
-      VecIO<T, VEC>::load(word + e0, w);
-      if (pos) VecIO<T, VEC>::load(pos + e0, q);
-      if (typ) VecIO<T, VEC>::load(typ + e0, y);
+    const bool in = (k * WAVE + lane) * VEC < N;
 #pragma unroll
-      for (int i = 0; i < VEC; i++) v[k][i] = (w[i] + (pos ? q[i] : 0.f)) + (typ ? y[i] : 0.f);
-    } else {
-#pragma unroll
-      for (int i = 0; i < VEC; i++) v[k][i] = 0.f;
-    }
+    for (int i = 0; i < VEC; i++) v[k][i] = in ? (w[k][i] + (pos ? q[k][i] : 0.f)) + (typ ? y[k][i] : 0.f) : 0.f;
   }
-  ln_finish<T, VEC, PER>(v, N, (const T *)a.gamma, (const T *)a.beta, a.eps, (T *)a.out + r * N, lane,
-                         a.row_scale ? a.row_scale + r : nullptr);
+  ln_finish_pre<T, VEC, PER>(v, N, gm, bt, a.beta != nullptr, a.eps, (T *)a.out + r * N, lane,
+                             a.row_scale ? a.row_scale + r : nullptr);
   prefetch_share(pf);
 }
 
