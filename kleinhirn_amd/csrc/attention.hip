@@ -200,8 +200,20 @@ attn_kernel(AttnArgs a, Packing p) {
   // sub-tile's work instead of stalling its c2p products
   [[maybe_unused]] frag_t pk_next[QS];
   if constexpr (REL) {
-    // visible to every wavefront after the first K/V staging barrier
-    for (int i = t; i < 2 * a.lmax - 1; i += 128) sBucket[i] = (short)a.bucket[i];
+    // visible to every wavefront after the first K/V staging barrier; 8 entries per thread are
+    // read before any is written (a loop of read, wait, write paid one round trip per entry)
+    const int nbk = 2 * a.lmax - 1;
+    for (int i0 = 0; i0 < nbk; i0 += 128 * 8) {
+      int bv[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int i = i0 + t + u * 128;
+        bv[u] = a.bucket[i < nbk ? i : nbk - 1];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (i0 + t + u * 128 < nbk) sBucket[i0 + t + u * 128] = (short)bv[u];
+    }
     c2p_carry = c2p_block(q0 + w * 32 - (klo + 31) + 32, std::false_type{});
     if constexpr (PQC) {
       pos_frags(a.pos_query, q0 + w * 32 - (klo + 31) + 32, pq_carry, std::false_type{});
