@@ -118,13 +118,19 @@ attn_kernel(AttnArgs a, Packing p) {
   // items (head, query tile), tiles fastest: the query tiles of one sequence and head run
   // together on one XCD and find its K and V rows in that XCD's L2
   const int H = a.H;
-  const int item = a.work ? a.work[blockIdx.x] : xcd_tile(blockIdx.x, a.ntiles * H);
-  if (item < 0) return;  // (the work list's padding: an XCD with fewer items)
-  const int4 tile = a.tiles[item % a.ntiles];
-  const int q0 = tile.y;
-  const int h = item / a.ntiles;
-  const int64_t base = tile.z;
-  const int n = tile.w;
+  int4 wk;  // {head, first query, first packed row, length}
+  if (a.work) {
+    wk = a.work[blockIdx.x];
+  } else {
+    const int item = xcd_tile(blockIdx.x, a.ntiles * H);
+    const int4 tile = a.tiles[item % a.ntiles];
+    wk = int4{item / a.ntiles, tile.y, tile.z, tile.w};
+  }
+  if (wk.x < 0) return;  // (the work list's padding: an XCD with fewer items)
+  const int q0 = wk.y;
+  const int h = wk.x;
+  const int64_t base = wk.z;
+  const int n = wk.w;
   const int64_t rs = (int64_t)3 * H * Dr;  // qkv row stride
   const int rs32 = 3 * H * Dr;
   const T *qkv = (const T *)a.qkv;

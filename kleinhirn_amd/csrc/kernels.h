@@ -155,9 +155,11 @@ struct AttnArgs {
   int lmax = 0;
   const int4 *tiles;
   int ntiles;
-  // the grid's blocks in dispatch order (null: item = xcd_tile(block)): block b runs item work[b]
-  // (item h * ntiles + tile; -1 for none), its blocks' XCD b % 8 (see the runner's attention order)
-  const int32_t *work = nullptr;
+  // the grid's blocks in dispatch order (null: item = xcd_tile(block)): block b runs work[b] =
+  // {head, first query, first packed row, length} of its query tile ({-1, 0, 0, 0} for none), its
+  // blocks' XCD b % 8 (see the runner's attention order); the tile itself is in the entry, so a
+  // block reads one entry before its rows
+  const int4 *work = nullptr;
   int nwork = 0;
 };
 void attention(bool f16, const AttnArgs &a, const Packing &p, hipStream_t s);

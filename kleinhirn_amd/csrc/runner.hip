@@ -956,7 +956,7 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook, const 
       a.tiles = (const int4 *)(s.first_tiles ? pl->d_tiles_first.p : pl->d_tiles.p);
       a.ntiles = s.first_tiles ? pl->ntiles_first : pl->ntiles;
       a.nwork = s.first_tiles ? pl->nwork_first : pl->nwork;
-      if (a.nwork > 0 && s.H == pl->work_h) a.work = (const int32_t *)(s.first_tiles ? pl->d_work_first.p : pl->d_work.p);
+      if (a.nwork > 0 && s.H == pl->work_h) a.work = (const int4 *)(s.first_tiles ? pl->d_work_first.p : pl->d_work.p);
       else a.nwork = 0;
       const double hd = (double)s.H * s.D;
       double pairs = s.first_tiles ? pl->attn_pairs_first : pl->attn_pairs_global;
@@ -990,7 +990,7 @@ static void exec_step(kh_plan *pl, const Step &s, const LaunchHook &hook, const 
 // the blocks that visit the most key tiles do not start last. A block's work is taken as its key
 // tiles plus a fixed cost: on a ragged batch the longest sequences' blocks visit several times the
 // key tiles of the others (c2: 3 against 1.4 on average; c4: 128 against 80).
-static std::vector<int32_t> attn_order(const std::vector<int4> &tiles, int H) {
+static std::vector<int4> attn_order(const std::vector<int4> &tiles, int H) {
   const int nt = (int)tiles.size();
   struct Group {
     double w;
@@ -1016,9 +1016,13 @@ static std::vector<int32_t> attn_order(const std::vector<int4> &tiles, int H) {
   }
   size_t len = 0;
   for (const auto &l : lists) len = std::max(len, l.size());
-  std::vector<int32_t> work(8 * len, -1);
+  std::vector<int4> work(8 * len, int4{-1, 0, 0, 0});
   for (int x = 0; x < 8; x++)
-    for (size_t i = 0; i < lists[x].size(); i++) work[x + 8 * i] = lists[x][i];
+    for (size_t i = 0; i < lists[x].size(); i++) {
+      const int item = lists[x][i];
+      const int4 &t = tiles[item % nt];
+      work[x + 8 * i] = int4{item / nt, t.y, t.z, t.w};
+    }
   return work;
 }
 
@@ -1091,7 +1095,7 @@ static void pack(kh_plan *pl, int rows, int b_end) {
   int H = 0;
   for (const Step &s : pl->steps)
     if (s.kind == S_ATTN && H == 0) H = s.H;
-  std::vector<int32_t> work, work_first;
+  std::vector<int4> work, work_first;
   if (H > 0) {
     work = attn_order(tiles, H);
     work_first = attn_order(tiles_first, H);
@@ -1108,15 +1112,16 @@ static void pack(kh_plan *pl, int rows, int b_end) {
   if (pl->d_tiles.bytes < tiles.size() * sizeof(int4) || !pl->d_tiles.p) pl->d_tiles.alloc(tiles.size() * sizeof(int4));
   if (pl->d_tiles_first.bytes < tiles_first.size() * sizeof(int4) || !pl->d_tiles_first.p)
     pl->d_tiles_first.alloc(tiles_first.size() * sizeof(int4));
-  if (!work.empty() && (pl->d_work.bytes < work.size() * 4 || !pl->d_work.p)) pl->d_work.alloc(work.size() * 4);
-  if (!work_first.empty() && (pl->d_work_first.bytes < work_first.size() * 4 || !pl->d_work_first.p))
-    pl->d_work_first.alloc(work_first.size() * 4);
+  if (!work.empty() && (pl->d_work.bytes < work.size() * sizeof(int4) || !pl->d_work.p))
+    pl->d_work.alloc(work.size() * sizeof(int4));
+  if (!work_first.empty() && (pl->d_work_first.bytes < work_first.size() * sizeof(int4) || !pl->d_work_first.p))
+    pl->d_work_first.alloc(work_first.size() * sizeof(int4));
   KH_CHECK(hipStreamSynchronize(pl->stream));  // staging may still feed an earlier copy
   // ten blocks at most (cu, row_pos, row_seq, tiles, first tiles, the two work lists, type ids,
   // ids, markers), each 16-byte aligned
   const size_t T1 = (size_t)std::max<int64_t>(T, 1);
   const size_t meta = (size_t)(B + 1) * 4 + 5 * T1 * 4 + (tiles.size() + tiles_first.size()) * sizeof(int4) +
-                      (work.size() + work_first.size()) * 4 + pl->markers_host.size() * 4 + 11 * 16;
+                      (work.size() + work_first.size()) * sizeof(int4) + pl->markers_host.size() * 4 + 11 * 16;
   pl->pin_meta.ensure(meta);
   char *mp = (char *)pl->pin_meta.p;
   char *const mend = mp + meta;
@@ -1131,8 +1136,8 @@ static void pack(kh_plan *pl, int rows, int b_end) {
   put(pl->d_row_seq, row_seq.data(), (size_t)std::max<int64_t>(T, 1) * 4);
   put(pl->d_tiles, tiles.data(), tiles.size() * sizeof(int4));
   put(pl->d_tiles_first, tiles_first.data(), tiles_first.size() * sizeof(int4));
-  if (!work.empty()) put(pl->d_work, work.data(), work.size() * 4);
-  if (!work_first.empty()) put(pl->d_work_first, work_first.data(), work_first.size() * 4);
+  if (!work.empty()) put(pl->d_work, work.data(), work.size() * sizeof(int4));
+  if (!work_first.empty()) put(pl->d_work_first, work_first.data(), work_first.size() * sizeof(int4));
   pl->masked = masked;
   if (masked) {
     std::vector<float> w(T1, 0.f);
