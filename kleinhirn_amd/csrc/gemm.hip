@@ -636,8 +636,9 @@ __device__ __forceinline__ rsrc_t panel_rsrc(const void *base, uint32_t bytes) {
 // The bias values of this wavefront's accumulator columns, loaded once before the k loop so the
 // epilogue waits for no load: bv[j][q] holds the 4 values of columns wn TN + 32 j + 8 q + 4 lg
 // (+ 0..3), or for GeGLU those of the rows of W the tile's two halves take (columns n0 / 2 + c of
-// each half of the product). Columns past N read column 0 and are zeroed: every lane loads, so
-// the loads go out together instead of one conditional load (and its wait) per column group.
+// each half of the product). Every lane loads, so the loads go out together; columns past N read
+// column 0's values, which only reach outputs the store phase drops (nothing reads the loaded
+// values here, so no wait for them comes before the k loop).
 template <int BN, int WN, int EPI, int FN>
 __device__ __forceinline__ void lean_bias(const GemmArgs &g, int n0, int wn, int lane, half4v (&bv)[FN][4]) {
   constexpr int TN = BN / WN;
@@ -650,12 +651,7 @@ __device__ __forceinline__ void lean_bias(const GemmArgs &g, int n0, int wn, int
       const int nl = wn * TN + j * 32 + 8 * q;
       int n = n0 + nl + 4 * lg;
       if constexpr (EPI == EPI_GEGLU) n = (nl < BN / 2 ? (n0 >> 1) + nl : g.N / 2 + (n0 >> 1) + nl - BN / 2) + 4 * lg;
-      half4v b = {};
-      if (bias) {
-        b = *reinterpret_cast<const half4v *>(bias + (n < g.N ? n : 0));
-        if (n >= g.N) b = half4v{};
-      }
-      bv[j][q] = b;
+      bv[j][q] = bias ? *reinterpret_cast<const half4v *>(bias + (n < g.N ? n : 0)) : half4v{};
     }
 }
 
