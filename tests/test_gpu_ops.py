@@ -79,7 +79,7 @@ def close(got, want, tol, what):
 @pytest.mark.parametrize("N,K,lens", [(384, 768, [5, 130]), (2304, 768, [257]), (37, 64, [7, 3]),
                                       (3, 768, [1, 4]), (1536, 384, [64, 64, 1]), (200, 136, [129]),
                                       (768, 3072, [300, 77]), (3072, 768, [193]), (768, 768, [1]),
-                                      (2, 768, [3, 1]), (3, 40, [2])])
+                                      (2, 768, [3, 1]), (3, 40, [2]), (200, 768, [129]), (264, 512, [70, 3])])
 def test_matmul_against_f64(f16, N, K, lens):
     L = max(lens)
     B = len(lens)
@@ -99,12 +99,14 @@ def test_matmul_against_f64(f16, N, K, lens):
         assert np.all(out[~valid] == 0), "padding rows must read back as zero"
 
 
+@pytest.mark.parametrize("N,K", [(768, 1536), (200, 768)])
 @pytest.mark.parametrize("tile", list(range(15)))
-def test_matmul_every_tile_configuration(tile, monkeypatch):
+def test_matmul_every_tile_configuration(tile, N, K, monkeypatch):
     """Each GEMM tile configuration (forced through KH_GEMM_TILE) on a ragged f16 batch whose rows
-    end inside a tile, against f64."""
+    end inside a tile, against f64; N = 200 also ends inside a column tile of every width (the
+    columns past N, whose bias reads are not used, are never stored)."""
     monkeypatch.setenv("KH_GEMM_TILE", str(tile))
-    N, K, lens = 768, 1536, [211, 5, 64]
+    lens = [211, 5, 64]
     L, B = max(lens), len(lens)
     W = (RNG.standard_normal((N, K)) * 0.05).astype(np.float16)
     bias = (RNG.standard_normal(N) * 0.1).astype(np.float16)
